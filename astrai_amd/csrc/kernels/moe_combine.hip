@@ -1,0 +1,148 @@
+// Weighted un-permute and combine.
+//
+// Reference semantics (astrai/model/components/mlp.py):
+//   :89  output = zeros(N, D)
+//   :98  for e ascending: output.index_add_(0, token_idx, y_e * w)  — each add
+//        rounds to x.dtype; a token meets each of its experts once
+//   :77  shared_out = sum(e(x) for e in shared_experts) / n_shared — Python's
+//        sum starts from 0 and rounds after every add; torch divides a tensor
+//        by a Python number as a multiply by the float reciprocal
+//        (1.0f / n_shared), rounded to x.dtype
+//   :71  out = shared_out + routed_out (shared_out = zeros when there are no
+//        shared experts, mlp.py:75-76)
+// The rows y already carry the routing weight (fused into the down GEMM).
+// Expert order equals ascending permuted-row order (rows are expert-major),
+// so each token's top_k row indices are sorted and summed in that order,
+// rounding after every add, then added to the shared output. Results are
+// bit-identical to the reference's sequence of bf16/fp32 adds.
+//
+// One wave per token; lanes stream the row with 16-byte vectors.
+#include "moe_common.h"
+
+namespace astrai_moe {
+namespace {
+
+constexpr int kCombineThreads = 256;
+constexpr int kTokensPerBlock = kCombineThreads / 64;
+
+template <typename T, int VW>
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(
+    const T* __restrict__ y, const int32_t* __restrict__ token_pos,
+    const T* __restrict__ shared, int n_shared, float inv_shared,
+    int64_t n_tokens, int top_k, int64_t dim, T* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * kTokensPerBlock + (threadIdx.x >> 6);
+  if (t >= n_tokens) return;
+
+  // Lane k < top_k holds row k; rank rows by position (distinct values, an
+  // invalid -1 sorts first and is skipped).
+  const int my_pos = lane < top_k ? token_pos[t * top_k + lane] : 0x7fffffff;
+  int rank = 0;
+  for (int k = 0; k < top_k; ++k) {
+    const int o = __shfl(my_pos, k, 64);
+    rank += (o < my_pos) ? 1 : 0;
+  }
+  int rows[ASTRAI_MOE_MAX_TOPK];
+#pragma unroll
+  for (int r = 0; r < ASTRAI_MOE_MAX_TOPK; ++r) {
+    if (r < top_k) {
+      // m is wave-uniform; duplicate positions leave some rank unclaimed.
+      const uint64_t m = __ballot(lane < top_k && rank == r);
+      const int src = m ? (int)(__ffsll((unsigned long long)m) - 1) : 0;
+      const int p = __shfl(my_pos, src, 64);
+      rows[r] = (m && p < n_tokens * top_k) ? p : -1;
+    }
+  }
+
+  const int64_t nvec = dim / VW;
+  for (int64_t v = lane; v < nvec; v += 64) {
+    float acc[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < ASTRAI_MOE_MAX_TOPK; ++r) {
+      if (r < top_k && rows[r] >= 0) {
+        const T* src = y + (int64_t)rows[r] * dim + v * VW;
+        T vals[VW];
+        if (VW * sizeof(T) == 16)
+          *reinterpret_cast<uint4*>(vals) = *reinterpret_cast<const uint4*>(src);
+        else
+#pragma unroll
+          for (int j = 0; j < VW; ++j) vals[j] = src[j];
+#pragma unroll
+        for (int j = 0; j < VW; ++j)
+          acc[j] = Elem<T>::round(acc[j] + Elem<T>::to_f32(vals[j]));
+      }
+    }
+    float sh[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) sh[j] = 0.0f;
+    for (int si = 0; si < n_shared; ++si) {
+      const T* sp = shared + ((int64_t)si * n_tokens + t) * dim + v * VW;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sh[j] = Elem<T>::round(sh[j] + Elem<T>::to_f32(sp[j]));
+    }
+    if (n_shared > 0)
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sh[j] = Elem<T>::round(sh[j] * inv_shared);
+    T res[VW];
+#pragma unroll
+    for (int j = 0; j < VW; ++j) res[j] = Elem<T>::from_f32(sh[j] + acc[j]);
+    T* dst = out + t * dim + v * VW;
+    if (VW * sizeof(T) == 16)
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(res);
+    else
+#pragma unroll
+      for (int j = 0; j < VW; ++j) dst[j] = res[j];
+  }
+}
+
+template <typename T>
+int launch_combine(const void* y, const int32_t* token_pos, const void* shared,
+                   int n_shared, int64_t n_tokens, int top_k, int64_t dim,
+                   void* out, hipStream_t s) {
+  const float inv_shared = n_shared > 0 ? 1.0f / (float)n_shared : 0.0f;
+  const unsigned grid = (unsigned)ceil_div(n_tokens, kTokensPerBlock);
+  constexpr int kVW = 16 / sizeof(T);
+  const bool vec = dim % kVW == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                   (!shared || reinterpret_cast<uintptr_t>(shared) % 16 == 0);
+  if (vec)
+    hipLaunchKernelGGL((combine_kernel<T, kVW>), dim3(grid), dim3(kCombineThreads),
+                       0, s, static_cast<const T*>(y), token_pos,
+                       static_cast<const T*>(shared), n_shared, inv_shared,
+                       n_tokens, top_k, dim, static_cast<T*>(out));
+  else
+    hipLaunchKernelGGL((combine_kernel<T, 1>), dim3(grid), dim3(kCombineThreads),
+                       0, s, static_cast<const T*>(y), token_pos,
+                       static_cast<const T*>(shared), n_shared, inv_shared,
+                       n_tokens, top_k, dim, static_cast<T*>(out));
+  return check_launch("combine_kernel");
+}
+
+}  // namespace
+}  // namespace astrai_moe
+
+using namespace astrai_moe;
+
+extern "C" int astrai_moe_combine(const void* y, const int32_t* token_pos,
+                                  const void* shared, int n_shared, int dtype,
+                                  int64_t n_tokens, int top_k, int64_t dim,
+                                  void* out, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(n_tokens >= 0, "combine: n_tokens must be >= 0");
+  ASTRAI_REQUIRE(top_k >= 1 && top_k <= ASTRAI_MOE_MAX_TOPK,
+                 "combine: top_k must be in [1, %d] (got %d)",
+                 ASTRAI_MOE_MAX_TOPK, top_k);
+  ASTRAI_REQUIRE(dim >= 1, "combine: dim must be >= 1");
+  if (n_tokens == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(y && token_pos && out, "combine: null buffer");
+  ASTRAI_REQUIRE(n_shared >= 0 && (n_shared == 0 || shared),
+                 "combine: n_shared must be >= 0 with a buffer when > 0");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ASTRAI_MOE_BF16)
+    return launch_combine<bf16_t>(y, token_pos, shared, n_shared, n_tokens, top_k, dim, out, s);
+  if (dtype == ASTRAI_MOE_F32)
+    return launch_combine<float>(y, token_pos, shared, n_shared, n_tokens, top_k, dim, out, s);
+  return fail(ASTRAI_MOE_EINVAL, "combine: unsupported dtype %d", dtype);
+}

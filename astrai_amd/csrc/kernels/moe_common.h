@@ -1,0 +1,88 @@
+// Shared device helpers and host error plumbing for libastrai_moe.so.
+// Target: gfx950 (CDNA4), wave64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "astrai_moe.h"
+
+namespace astrai_moe {
+
+typedef uint16_t bf16_t;  // bfloat16 bit pattern
+
+// ---------------------------------------------------------------------------
+// bfloat16 <-> float. Rounding is round-to-nearest-even with NaN mapped to the
+// quiet NaN 0x7FC0, which is what torch's float -> bfloat16 cast produces, so
+// every rounding point below lands on the same bits as the torch ops of
+// astrai/model/components/mlp.py.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline float bf16_bits_to_f32(bf16_t v) {
+  union {
+    uint32_t u;
+    float f;
+  } c;
+  c.u = (uint32_t)v << 16;
+  return c.f;
+}
+
+__host__ __device__ inline bf16_t f32_to_bf16_bits(float f) {
+  union {
+    uint32_t u;
+    float f;
+  } c;
+  c.f = f;
+  uint32_t u = c.u;
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// Element traits: storage type T, arithmetic in float. `round` maps a float
+// to the nearest value representable in T (identity for float).
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static constexpr int kDtype = ASTRAI_MOE_F32;
+  __device__ static inline float to_f32(float v) { return v; }
+  __device__ static inline float from_f32(float v) { return v; }
+  __device__ static inline float round(float v) { return v; }
+};
+
+template <>
+struct Elem<bf16_t> {
+  static constexpr int kDtype = ASTRAI_MOE_BF16;
+  __device__ static inline float to_f32(bf16_t v) { return bf16_bits_to_f32(v); }
+  __device__ static inline bf16_t from_f32(float v) { return f32_to_bf16_bits(v); }
+  __device__ static inline float round(float v) {
+    return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  }
+};
+
+// SiLU as torch evaluates it for float and for bfloat16 (opmath float):
+// x / (1 + exp(-x)).
+__device__ inline float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) {
+  return (a + b - 1) / b;
+}
+
+// ---------------------------------------------------------------------------
+// Host side: per-thread error message and launch checking (capi.hip).
+// ---------------------------------------------------------------------------
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+void clear_error();
+
+inline int64_t n_chunks(int64_t n_tokens) {
+  return ceil_div(n_tokens, ASTRAI_MOE_CHUNK_TOKENS);
+}
+
+}  // namespace astrai_moe
+
+#define ASTRAI_REQUIRE(cond, ...)                                  \
+  do {                                                             \
+    if (!(cond)) return ::astrai_moe::fail(ASTRAI_MOE_EINVAL, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,32 @@
+// Internal interface between the grouped-GEMM entry points (moe_gemm.hip) and
+// the CDNA4 matrix-core kernels (moe_gemm_mfma.hip).
+#pragma once
+
+#include "moe_common.h"
+
+namespace astrai_moe {
+
+// Row-tile heights of the bf16 matrix-core kernels. The large tile serves
+// prefill-sized expert loads; the small one serves decode-sized loads, where
+// the work is streaming expert weights and padding rows to 256 would make the
+// kernel compute-bound on empty rows.
+constexpr int kMfmaBigBM = 256;
+constexpr int kMfmaSmallBM = 32;
+
+// Shape constraints of the bf16 kernels: K a multiple of 64, the output
+// columns a multiple of the column tile, 16-byte aligned operands.
+bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m,
+                            const void* a, const void* c);
+bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m,
+                         const void* a, const void* c);
+
+int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles,
+                        int64_t capacity, const void* const* w_gate,
+                        const void* const* w_up, int64_t dim, int64_t dim_ffn,
+                        int block_m, void* h, hipStream_t s);
+int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
+                     const void* const* w_down, const void* sorted_w,
+                     int64_t dim_ffn, int64_t dim, int block_m, void* y,
+                     hipStream_t s);
+
+}  // namespace astrai_moe

@@ -1,0 +1,212 @@
+// Grouped expert GEMMs: entry points, tile scheduling and the general-shape
+// kernel.
+//
+// Reference semantics (astrai/model/components/mlp.py:22-25, :96-97):
+//   gated = up(x) * silu(gate(x))        (GEMM 1, rounded to x.dtype after
+//                                          gate, up, silu and the product)
+//   y     = down(gated) * w               (GEMM 2, rounded after down and
+//                                          after the weight product)
+// applied to every expert's rows of the permuted activations. nn.Linear
+// weights are [out, in] (astrai/model/components/linear.py:12), so both GEMMs
+// are C[rows, N] = A[rows, K] . W[N, K]^T with both operands K-contiguous.
+//
+// Work decomposition: one workgroup per (row tile, column tile). Row tiles
+// come from the device-built tile list (astrai_moe_permute), so the grid is
+// sized by the tile-list capacity and workgroups past the live tile count exit
+// at once; skewed and empty experts cost nothing beyond their own tiles.
+//
+// Kernels:
+//   * gemm_mfma_* (moe_gemm_mfma.hip): bf16 on CDNA4 matrix cores, used when
+//     the shapes meet its tiling constraints.
+//   * gemm_generic_kernel (here): any shape, fp32 or bf16, fp32 FMA; 64x64
+//     output tiles walked over the row tile in 64-row steps. Used for fp32 and
+//     for shapes the MFMA kernel does not tile.
+#include "moe_common.h"
+#include "moe_gemm.h"
+
+namespace astrai_moe {
+namespace {
+
+constexpr int kGenThreads = 256;
+constexpr int kGenBM = 64;
+constexpr int kGenBN = 64;
+constexpr int kGenBK = 16;
+
+template <typename T, bool kGateUp>
+__global__ __launch_bounds__(kGenThreads) void gemm_generic_kernel(
+    const T* __restrict__ A, const int32_t* __restrict__ tiles,
+    const void* const* __restrict__ W0, const void* const* __restrict__ W1,
+    const T* __restrict__ row_w, int64_t K, int64_t N, T* __restrict__ C) {
+  const int tile = blockIdx.x;
+  const int n_live = min(tiles[0], tiles[2]);
+  if (tile >= n_live) return;
+  const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)tile * ASTRAI_MOE_TILE_STRIDE;
+  const int e = ti[0];
+  const int64_t row0 = ti[1];
+  const int64_t rows_total = min((int64_t)tiles[1], (int64_t)ti[2] - row0);
+  const T* B0 = static_cast<const T*>(W0[e]);
+  const T* B1 = kGateUp ? static_cast<const T*>(W1[e]) : nullptr;
+  const int64_t n0 = (int64_t)blockIdx.y * kGenBN;
+
+  __shared__ float As[kGenBK][kGenBM + 1];
+  __shared__ float Bs0[kGenBK][kGenBN + 1];
+  __shared__ float Bs1[kGateUp ? kGenBK : 1][kGateUp ? kGenBN + 1 : 1];
+
+  const int tx = threadIdx.x % 16;
+  const int ty = threadIdx.x / 16;
+  for (int64_t rs = 0; rs < rows_total; rs += kGenBM) {
+    float acc0[4][4], acc1[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc0[i][j] = acc1[i][j] = 0.0f;
+
+    for (int64_t k0 = 0; k0 < K; k0 += kGenBK) {
+#pragma unroll
+      for (int j = 0; j < (kGenBM * kGenBK) / kGenThreads; ++j) {
+        const int idx = threadIdx.x + j * kGenThreads;
+        const int r = idx / kGenBK;
+        const int kk = idx % kGenBK;
+        const int64_t gk = k0 + kk;
+        const bool kin = gk < K;
+        As[kk][r] = (rs + r < rows_total && kin)
+                        ? Elem<T>::to_f32(A[(row0 + rs + r) * K + gk]) : 0.0f;
+        const int64_t n = n0 + r;
+        Bs0[kk][r] = (n < N && kin) ? Elem<T>::to_f32(B0[n * K + gk]) : 0.0f;
+        if (kGateUp)
+          Bs1[kk][r] = (n < N && kin) ? Elem<T>::to_f32(B1[n * K + gk]) : 0.0f;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int kk = 0; kk < kGenBK; ++kk) {
+        float a[4], b0[4], b1[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = As[kk][ty * 4 + i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          b0[j] = Bs0[kk][tx * 4 + j];
+          if (kGateUp) b1[j] = Bs1[kk][tx * 4 + j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            acc0[i][j] = fmaf(a[i], b0[j], acc0[i][j]);
+            if (kGateUp) acc1[i][j] = fmaf(a[i], b1[j], acc1[i][j]);
+          }
+      }
+      __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t r = rs + ty * 4 + i;
+      if (r >= rows_total) continue;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t n = n0 + tx * 4 + j;
+        if (n >= N) continue;
+        float v;
+        if (kGateUp) {
+          const float g = Elem<T>::round(acc0[i][j]);
+          const float u = Elem<T>::round(acc1[i][j]);
+          const float s = Elem<T>::round(silu_f32(g));
+          v = u * s;
+        } else {
+          v = Elem<T>::round(acc0[i][j]) * Elem<T>::to_f32(row_w[row0 + r]);
+        }
+        C[(row0 + r) * N + n] = Elem<T>::from_f32(v);
+      }
+    }
+  }
+}
+
+template <typename T, bool kGateUp>
+int launch_generic(const void* A, const int32_t* tiles, int64_t capacity,
+                   const void* const* W0, const void* const* W1,
+                   const void* row_w, int64_t K, int64_t N, void* C,
+                   hipStream_t s) {
+  if (capacity == 0) return ASTRAI_MOE_OK;
+  const dim3 grid((unsigned)capacity, (unsigned)ceil_div(N, kGenBN));
+  hipLaunchKernelGGL((gemm_generic_kernel<T, kGateUp>), grid, dim3(kGenThreads), 0,
+                     s, static_cast<const T*>(A), tiles, W0, W1,
+                     static_cast<const T*>(row_w), K, N, static_cast<T*>(C));
+  return check_launch(kGateUp ? "gemm_generic_kernel<gate_up>"
+                              : "gemm_generic_kernel<down>");
+}
+
+int check_common(const char* who, const void* A, const int32_t* tiles,
+                 int64_t tiles_len, int dtype, int64_t n_rows, int n_experts,
+                 int64_t K, int64_t N, int block_m, const void* C) {
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16 || dtype == ASTRAI_MOE_F32,
+                 "%s: unsupported dtype %d", who, dtype);
+  ASTRAI_REQUIRE(n_rows >= 0 && n_rows < (1ll << 31),
+                 "%s: n_rows must be in [0, 2^31) (got %lld)", who,
+                 (long long)n_rows);
+  ASTRAI_REQUIRE(n_experts >= 1 && n_experts <= ASTRAI_MOE_MAX_EXPERTS,
+                 "%s: n_experts must be in [1, %d] (got %d)", who,
+                 ASTRAI_MOE_MAX_EXPERTS, n_experts);
+  ASTRAI_REQUIRE(K >= 1 && N >= 1, "%s: dims must be >= 1", who);
+  ASTRAI_REQUIRE(block_m >= 1, "%s: block_m must be >= 1", who);
+  ASTRAI_REQUIRE(tiles_len >= ASTRAI_MOE_TILE_HEADER,
+                 "%s: tile list too short", who);
+  if (n_rows > 0) ASTRAI_REQUIRE(A && tiles && C, "%s: null buffer", who);
+  return ASTRAI_MOE_OK;
+}
+
+}  // namespace
+}  // namespace astrai_moe
+
+using namespace astrai_moe;
+
+extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
+                                       int64_t tiles_len,
+                                       const void* const* w_gate,
+                                       const void* const* w_up, int dtype,
+                                       int64_t n_rows, int n_experts,
+                                       int64_t dim, int64_t dim_ffn,
+                                       int block_m, void* h, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_gate_up", x_perm, tiles, tiles_len, dtype, n_rows,
+                        n_experts, dim, dim_ffn, block_m, h);
+  if (rc) return rc;
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_gate && w_up, "gemm_gate_up: null weight table");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ASTRAI_MOE_BF16) {
+    if (mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h))
+      return launch_mfma_gate_up(x_perm, tiles, capacity, w_gate, w_up, dim,
+                                 dim_ffn, block_m, h, s);
+    return launch_generic<bf16_t, true>(x_perm, tiles, capacity, w_gate, w_up,
+                                        nullptr, dim, dim_ffn, h, s);
+  }
+  return launch_generic<float, true>(x_perm, tiles, capacity, w_gate, w_up,
+                                     nullptr, dim, dim_ffn, h, s);
+}
+
+extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
+                                    int64_t tiles_len,
+                                    const void* const* w_down,
+                                    const void* sorted_w, int dtype,
+                                    int64_t n_rows, int n_experts,
+                                    int64_t dim_ffn, int64_t dim, int block_m,
+                                    void* y, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_down", h, tiles, tiles_len, dtype, n_rows,
+                        n_experts, dim_ffn, dim, block_m, y);
+  if (rc) return rc;
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_down && sorted_w, "gemm_down: null weight table or row weights");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ASTRAI_MOE_BF16) {
+    if (mfma_down_supported(dim_ffn, dim, block_m, h, y))
+      return launch_mfma_down(h, tiles, capacity, w_down, sorted_w, dim_ffn,
+                              dim, block_m, y, s);
+    return launch_generic<bf16_t, false>(h, tiles, capacity, w_down, nullptr,
+                                         sorted_w, dim_ffn, dim, y, s);
+  }
+  return launch_generic<float, false>(h, tiles, capacity, w_down, nullptr,
+                                      sorted_w, dim_ffn, dim, y, s);
+}

@@ -1,0 +1,303 @@
+// Token permutation by expert (a counting sort keyed on expert id).
+//
+// Reference semantics (astrai/model/components/mlp.py:90-95): for each expert
+// e in ascending order, (topk_idx == e).nonzero() lists the tokens routed to e
+// in ascending token order and x[token_idx] gathers their rows. The permuted
+// row order is the concatenation over experts, so it is fixed exactly:
+// expert-major, token-ascending. Integer work only; results are bit-exact.
+//
+// Two kernels:
+//   scan_kernel     one block. Column sums of the per-chunk histograms give
+//                   per-expert counts; a block-wide exclusive scan (wave64
+//                   shuffle scan + LDS for wave totals) gives expert offsets;
+//                   per-chunk bases give every chunk its first slot in each
+//                   expert's segment; the GEMM row-tile list is laid out from
+//                   the counts (tiles never straddle experts, empty experts
+//                   get none) so no host synchronisation is needed.
+//   scatter_kernel  one block per chunk. Wave 0 ranks the chunk's (token,
+//                   slot) entries in order: lanes holding the same expert are
+//                   found with one ballot per expert-id bit, the rank is the
+//                   popcount of lower peer lanes, and an LDS counter per
+//                   expert carries the running position. Then all waves copy
+//                   each token row once from x and write it to its top_k
+//                   destinations with 16-byte vector accesses.
+#include "moe_common.h"
+
+namespace astrai_moe {
+namespace {
+
+constexpr int kScanThreads = 1024;
+constexpr int kScatterThreads = 256;
+
+// Inclusive scan of `v` over the block (blockDim.x == kScanThreads).
+__device__ int block_inclusive_scan(int v, int* s_wave) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  if (lane == 63) s_wave[wave] = v;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < kScanThreads / 64 ? s_wave[lane] : 0;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int o = __shfl_up(w, off, 64);
+      if (lane >= off) w += o;
+    }
+    if (lane < kScanThreads / 64) s_wave[lane] = w;
+  }
+  __syncthreads();
+  const int r = v + (wave > 0 ? s_wave[wave - 1] : 0);
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(
+    const int32_t* __restrict__ chunk_hist, int64_t n_chunks_, int n_experts,
+    int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ chunk_base, int32_t* __restrict__ tiles) {
+  __shared__ int s_part[kScanThreads];
+  __shared__ int s_wave[kScanThreads / 64];
+  __shared__ int s_off[ASTRAI_MOE_MAX_EXPERTS];
+
+  // Threads form a [splits][ep] grid: ep = next_pow2(E) expert columns, each
+  // column's chunks split into `splits` contiguous ranges.
+  int ep = 1;
+  while (ep < n_experts) ep *= 2;
+  const int splits = kScanThreads / ep;
+  const int e = threadIdx.x % ep;
+  const int s = threadIdx.x / ep;
+  const int64_t per = ceil_div(n_chunks_, splits);
+  const int64_t c0 = min((int64_t)s * per, n_chunks_);
+  const int64_t c1 = min(c0 + per, n_chunks_);
+
+  int local = 0;
+  if (e < n_experts)
+    for (int64_t c = c0; c < c1; ++c) local += chunk_hist[c * n_experts + e];
+  s_part[threadIdx.x] = local;
+  __syncthreads();
+  // Exclusive prefix over the splits of each expert column.
+  if (s == 0) {
+    int run = 0;
+    for (int j = 0; j < splits; ++j) {
+      const int v = s_part[j * ep + e];
+      s_part[j * ep + e] = run;
+      run += v;
+    }
+    s_off[e] = e < n_experts ? run : 0;
+  }
+  __syncthreads();
+
+  // Expert offsets and tile starts: block scans over expert ids.
+  const int cnt = (threadIdx.x < n_experts) ? s_off[threadIdx.x] : 0;
+  const int ntile = (cnt + block_m - 1) / block_m;
+  const int cnt_incl = block_inclusive_scan(cnt, s_wave);
+  const int tile_incl = block_inclusive_scan(ntile, s_wave);
+  const int off = cnt_incl - cnt;
+  const int tile0 = tile_incl - ntile;
+  if (threadIdx.x < n_experts) {
+    expert_offsets[threadIdx.x] = off;
+    if (threadIdx.x == n_experts - 1) {
+      expert_offsets[n_experts] = cnt_incl;
+      tiles[0] = tile_incl;
+      tiles[1] = block_m;
+      tiles[2] = (int32_t)tile_capacity;
+      tiles[3] = 0;
+    }
+    for (int j = 0; j < ntile && tile0 + j < tile_capacity; ++j) {
+      int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER +
+                   (int64_t)(tile0 + j) * ASTRAI_MOE_TILE_STRIDE;
+      t[0] = threadIdx.x;
+      t[1] = off + j * block_m;
+      t[2] = off + cnt;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < n_experts) s_off[threadIdx.x] = off;
+  __syncthreads();
+
+  // Chunk bases: expert offset + tokens of that expert in earlier chunks.
+  if (e < n_experts) {
+    int run = s_off[e] + s_part[threadIdx.x];
+    for (int64_t c = c0; c < c1; ++c) {
+      const int v = chunk_hist[c * n_experts + e];
+      chunk_base[c * n_experts + e] = run;
+      run += v;
+    }
+  }
+}
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
+    const int32_t* __restrict__ topk_idx, const T* __restrict__ topk_w,
+    const int32_t* __restrict__ chunk_base, const T* __restrict__ x,
+    int64_t n_tokens, int n_experts, int top_k, int64_t dim,
+    int32_t* __restrict__ sorted_token, T* __restrict__ sorted_w,
+    int32_t* __restrict__ token_pos, T* __restrict__ x_perm) {
+  __shared__ int cnt[ASTRAI_MOE_MAX_EXPERTS];
+  __shared__ int pos_l[ASTRAI_MOE_CHUNK_TOKENS * ASTRAI_MOE_MAX_TOPK];
+  const int64_t chunk = blockIdx.x;
+  const int64_t t0 = chunk * ASTRAI_MOE_CHUNK_TOKENS;
+  const int nt = (int)min((int64_t)ASTRAI_MOE_CHUNK_TOKENS, n_tokens - t0);
+  const int n_ent = nt * top_k;
+  const int64_t n_rows = n_tokens * top_k;
+  for (int e = threadIdx.x; e < n_experts; e += kScatterThreads)
+    cnt[e] = chunk_base[chunk * n_experts + e];
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x < 64) {
+    int nbits = 0;
+    while ((1 << nbits) < n_experts) ++nbits;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = 0; base < n_ent; base += 64) {
+      const int i = base + lane;
+      int e = i < n_ent ? topk_idx[t0 * top_k + i] : -1;
+      const bool valid = e >= 0 && e < n_experts;
+      uint64_t peers = __ballot(valid);
+      for (int b = 0; b < nbits; ++b) {
+        const bool bit = valid && ((e >> b) & 1);
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      const int rank = __popcll(peers & lt_mask);
+      const int p = valid ? cnt[e] + rank : -1;
+      // All reads of cnt above complete before any update below (in-order
+      // LDS queue of one wave); the highest peer lane advances the counter.
+      const bool last = valid && (peers >> lane) == 1ull;
+      if (last) cnt[e] += __popcll(peers);
+      if (i < n_ent) {
+        const bool ok = valid && p >= 0 && p < n_rows;
+        pos_l[i] = ok ? p : -1;
+        token_pos[t0 * top_k + i] = ok ? p : -1;
+        if (ok) {
+          sorted_token[p] = (int32_t)(t0 + i / top_k);
+          sorted_w[p] = topk_w[t0 * top_k + i];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Row copy: each token row is read once and written top_k times.
+  const int wave = threadIdx.x >> 6;
+  constexpr int kWaves = kScatterThreads / 64;
+  if (kVec) {
+    // 16-byte vectors; dim * sizeof(T) is a multiple of 16.
+    const int64_t nvec = dim * (int64_t)sizeof(T) / 16;
+    for (int lt = wave; lt < nt; lt += kWaves) {
+      const uint4* src = reinterpret_cast<const uint4*>(x + (t0 + lt) * dim);
+      for (int64_t v = lane; v < nvec; v += 64) {
+        const uint4 val = src[v];
+        for (int k = 0; k < top_k; ++k) {
+          const int p = pos_l[lt * top_k + k];
+          if (p >= 0) reinterpret_cast<uint4*>(x_perm + (int64_t)p * dim)[v] = val;
+        }
+      }
+    }
+  } else {
+    for (int lt = wave; lt < nt; lt += kWaves) {
+      const T* src = x + (t0 + lt) * dim;
+      for (int64_t c = lane; c < dim; c += 64) {
+        const T val = src[c];
+        for (int k = 0; k < top_k; ++k) {
+          const int p = pos_l[lt * top_k + k];
+          if (p >= 0) x_perm[(int64_t)p * dim + c] = val;
+        }
+      }
+    }
+  }
+}
+
+template <typename T>
+int launch_permute(const int32_t* topk_idx, const void* topk_w,
+                   const int32_t* chunk_hist, const void* x, int64_t n_tokens,
+                   int n_experts, int top_k, int64_t dim, int block_m,
+                   int32_t* expert_offsets, int32_t* sorted_token,
+                   void* sorted_w, int32_t* token_pos, void* x_perm,
+                   int32_t* tiles, int64_t tile_capacity, int32_t* chunk_base,
+                   hipStream_t s) {
+  const int64_t nc = n_chunks(n_tokens);
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s, chunk_hist,
+                     nc, n_experts, block_m, tile_capacity, expert_offsets,
+                     chunk_base, tiles);
+  int rc = check_launch("scan_kernel");
+  if (rc || nc == 0) return rc;
+  const bool vec = (dim * (int64_t)sizeof(T)) % 16 == 0 &&
+                   (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
+                   (reinterpret_cast<uintptr_t>(x_perm) % 16) == 0;
+  if (vec)
+    hipLaunchKernelGGL((scatter_kernel<T, true>), dim3((unsigned)nc),
+                       dim3(kScatterThreads), 0, s, topk_idx,
+                       static_cast<const T*>(topk_w), chunk_base,
+                       static_cast<const T*>(x), n_tokens, n_experts, top_k,
+                       dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
+                       static_cast<T*>(x_perm));
+  else
+    hipLaunchKernelGGL((scatter_kernel<T, false>), dim3((unsigned)nc),
+                       dim3(kScatterThreads), 0, s, topk_idx,
+                       static_cast<const T*>(topk_w), chunk_base,
+                       static_cast<const T*>(x), n_tokens, n_experts, top_k,
+                       dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
+                       static_cast<T*>(x_perm));
+  return check_launch("scatter_kernel");
+}
+
+}  // namespace
+}  // namespace astrai_moe
+
+using namespace astrai_moe;
+
+extern "C" int64_t astrai_moe_tile_list_len(int64_t n_tokens, int n_experts,
+                                            int top_k, int block_m) {
+  if (n_tokens < 0 || n_experts < 1 || top_k < 1 || block_m < 1) return -1;
+  const int64_t rows = n_tokens * top_k;
+  int64_t cap = (rows + (int64_t)n_experts * (block_m - 1)) / block_m;
+  if (cap > rows) cap = rows;
+  return ASTRAI_MOE_TILE_HEADER + cap * ASTRAI_MOE_TILE_STRIDE;
+}
+
+extern "C" int astrai_moe_permute(
+    const int32_t* topk_idx, const void* topk_w, const int32_t* chunk_hist,
+    const void* x, int dtype, int64_t n_tokens, int n_experts, int top_k,
+    int64_t dim, int block_m, int32_t* expert_offsets, int32_t* sorted_token,
+    void* sorted_w, int32_t* token_pos, void* x_perm, int32_t* tiles,
+    int64_t tiles_len, int32_t* chunk_base, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(n_tokens >= 0 && n_tokens * (int64_t)top_k < (1ll << 31),
+                 "permute: n_tokens * top_k must be in [0, 2^31) (got %lld)",
+                 (long long)(n_tokens * (int64_t)top_k));
+  ASTRAI_REQUIRE(n_experts >= 1 && n_experts <= ASTRAI_MOE_MAX_EXPERTS,
+                 "permute: n_experts must be in [1, %d] (got %d)",
+                 ASTRAI_MOE_MAX_EXPERTS, n_experts);
+  ASTRAI_REQUIRE(top_k >= 1 && top_k <= n_experts && top_k <= ASTRAI_MOE_MAX_TOPK,
+                 "permute: top_k must be in [1, min(n_experts, %d)] (got %d)",
+                 ASTRAI_MOE_MAX_TOPK, top_k);
+  ASTRAI_REQUIRE(dim >= 1, "permute: dim must be >= 1");
+  ASTRAI_REQUIRE(block_m >= 1, "permute: block_m must be >= 1");
+  const int64_t need = astrai_moe_tile_list_len(n_tokens, n_experts, top_k, block_m);
+  ASTRAI_REQUIRE(tiles_len >= need,
+                 "permute: tile list holds %lld int32, needs %lld",
+                 (long long)tiles_len, (long long)need);
+  ASTRAI_REQUIRE(topk_idx && topk_w && chunk_hist && x && expert_offsets &&
+                     sorted_token && sorted_w && token_pos && x_perm && tiles &&
+                     chunk_base,
+                 "permute: null buffer");
+  const int64_t capacity =
+      (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ASTRAI_MOE_BF16)
+    return launch_permute<bf16_t>(topk_idx, topk_w, chunk_hist, x, n_tokens,
+                                  n_experts, top_k, dim, block_m, expert_offsets,
+                                  sorted_token, sorted_w, token_pos, x_perm, tiles,
+                                  capacity, chunk_base, s);
+  if (dtype == ASTRAI_MOE_F32)
+    return launch_permute<float>(topk_idx, topk_w, chunk_hist, x, n_tokens,
+                                 n_experts, top_k, dim, block_m, expert_offsets,
+                                 sorted_token, sorted_w, token_pos, x_perm, tiles,
+                                 capacity, chunk_base, s);
+  return fail(ASTRAI_MOE_EINVAL, "permute: unsupported dtype %d", dtype);
+}

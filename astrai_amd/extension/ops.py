@@ -1,0 +1,296 @@
+"""Tensor-level wrappers of the MoE HIP kernels — one function per entry point.
+
+Each wrapper validates its arguments in Python (``ValueError`` on bad input,
+as the reference's ``astrai/extension/ops.py:26-34,266-274`` does), allocates
+its outputs with torch's caching allocator on the inputs' device, and enqueues
+the kernel on the current stream through the C ABI (``include/astrai_moe.h``).
+Nothing here synchronises with the host.
+
+There is no torch fallback: a wrapper whose kernel is unavailable raises
+``RuntimeError`` (the reference's wrappers fall back to torch,
+``ops.py:180-190``; this package is the GPU path itself).
+
+Pipeline of the routed experts (``astrai/model/components/mlp.py:79-100``):
+
+    logits --moe_route--> (topk_idx, topk_w, chunk_hist)
+           --moe_permute--> (offsets, sorted rows, tile list, x_perm)
+           --moe_gemm_gate_up--> h = up(x) * silu(gate(x))
+           --moe_gemm_down--> y = down(h) * w
+           --moe_combine--> out
+"""
+
+from __future__ import annotations
+
+from typing import NamedTuple, Sequence
+
+import torch
+
+from astrai_amd.extension import loader
+from astrai_amd.extension.loader import _available, _modules
+
+CHUNK_TOKENS = 32  # ASTRAI_MOE_CHUNK_TOKENS
+MAX_EXPERTS = 1024
+MAX_TOPK = 32
+TILE_HEADER = 4
+TILE_STRIDE = 3
+
+_DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1}
+
+
+class RouteResult(NamedTuple):
+    topk_idx: torch.Tensor  # [T, K] int32, descending probability
+    topk_w: torch.Tensor  # [T, K] dtype, renormalised
+    chunk_hist: torch.Tensor  # [ceil(T / 32), E] int32
+
+
+class PermuteResult(NamedTuple):
+    expert_offsets: torch.Tensor  # [E + 1] int32
+    sorted_token: torch.Tensor  # [T*K] int32
+    sorted_w: torch.Tensor  # [T*K] dtype
+    token_pos: torch.Tensor  # [T, K] int32
+    x_perm: torch.Tensor  # [T*K, D] dtype
+    tiles: torch.Tensor  # tile list, int32
+    block_m: int
+
+
+def _kernel(name: str):
+    if not _available.get(name, False):
+        raise RuntimeError(f"MoE HIP kernel '{name}' unavailable: {loader.load_error()}")
+    return getattr(_modules[name], name)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {loader.last_error()}")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    code = _DTYPE_CODES.get(t.dtype)
+    if code is None:
+        raise ValueError(f"{name} must be float32 or bfloat16, got {t.dtype}")
+    return code
+
+
+def _require_gpu(t: torch.Tensor, name: str, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a ROCm device, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def select_block_m(n_tokens: int, n_experts: int, top_k: int, dim: int, dim_ffn: int, dtype: torch.dtype) -> int:
+    """Rows per GEMM tile the kernels use for this problem (host policy)."""
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
+        raise ValueError(f"unsupported dtype {dtype}")
+    bm = loader.library().astrai_moe_select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, code)
+    _check(0 if bm > 0 else bm, "select_block_m")
+    return bm
+
+
+def tile_list_len(n_tokens: int, n_experts: int, top_k: int, block_m: int) -> int:
+    n = loader.library().astrai_moe_tile_list_len(n_tokens, n_experts, top_k, block_m)
+    if n < 0:
+        raise ValueError("tile_list_len: bad sizes")
+    return n
+
+
+def expert_weight_table(weights: Sequence[torch.Tensor], shape: tuple[int, int]) -> torch.Tensor:
+    """Device array of the experts' weight pointers (int64), for the GEMMs.
+
+    Every weight must be a contiguous ``[out, in] == shape`` tensor on one
+    device with one dtype; the kernels read them in place.
+    """
+    if len(weights) == 0:
+        raise ValueError("no expert weights")
+    dev, dt = weights[0].device, weights[0].dtype
+    for i, w in enumerate(weights):
+        _require_gpu(w, f"expert weight {i}", 2)
+        if tuple(w.shape) != tuple(shape):
+            raise ValueError(f"expert weight {i} has shape {tuple(w.shape)}, expected {tuple(shape)}")
+        if w.device != dev or w.dtype != dt:
+            raise ValueError("expert weights must share one device and dtype")
+    return torch.tensor([w.data_ptr() for w in weights], dtype=torch.int64).to(dev)
+
+
+def moe_route(logits: torch.Tensor, top_k: int) -> RouteResult:
+    """Softmax, top-k and renormalisation of router logits (mlp.py:84-87)."""
+    fn = _kernel("moe_route")
+    _require_gpu(logits, "logits", 2)
+    code = _dtype_code(logits, "logits")
+    n_tokens, n_experts = logits.shape
+    if not 1 <= n_experts <= MAX_EXPERTS:
+        raise ValueError(f"n_experts must be in [1, {MAX_EXPERTS}], got {n_experts}")
+    if not 1 <= top_k <= min(n_experts, MAX_TOPK):
+        raise ValueError(f"top_k must be in [1, min(n_experts, {MAX_TOPK})], got {top_k}")
+    dev = logits.device
+    topk_idx = torch.empty(n_tokens, top_k, dtype=torch.int32, device=dev)
+    topk_w = torch.empty(n_tokens, top_k, dtype=logits.dtype, device=dev)
+    chunk_hist = torch.empty(-(-n_tokens // CHUNK_TOKENS), n_experts, dtype=torch.int32, device=dev)
+    _check(
+        fn(logits.data_ptr(), code, n_tokens, n_experts, top_k, topk_idx.data_ptr(), topk_w.data_ptr(),
+           chunk_hist.data_ptr(), _stream(logits)),
+        "moe_route",
+    )
+    return RouteResult(topk_idx, topk_w, chunk_hist)
+
+
+def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: int) -> PermuteResult:
+    """Expert-major, token-ascending permutation of the routed rows
+    (mlp.py:90-95) plus the device-built GEMM tile list."""
+    fn = _kernel("moe_permute")
+    _require_gpu(x, "x", 2)
+    code = _dtype_code(x, "x")
+    topk_idx, topk_w, chunk_hist = route
+    n_tokens, dim = x.shape
+    if topk_idx.shape[0] != n_tokens or topk_w.shape != topk_idx.shape:
+        raise ValueError("routing tensors do not match x")
+    if topk_w.dtype != x.dtype:
+        raise ValueError("topk_w must have x's dtype")
+    top_k = topk_idx.shape[1]
+    dev = x.device
+    rows = n_tokens * top_k
+    tl = tile_list_len(n_tokens, n_experts, top_k, block_m)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    sorted_token = torch.empty(rows, dtype=torch.int32, device=dev)
+    sorted_w = torch.empty(rows, dtype=x.dtype, device=dev)
+    token_pos = torch.empty(n_tokens, top_k, dtype=torch.int32, device=dev)
+    x_perm = torch.empty(rows, dim, dtype=x.dtype, device=dev)
+    tiles = torch.empty(tl, dtype=torch.int32, device=dev)
+    chunk_base = torch.empty_like(chunk_hist)
+    _check(
+        fn(topk_idx.data_ptr(), topk_w.data_ptr(), chunk_hist.data_ptr(), x.data_ptr(), code, n_tokens, n_experts,
+           top_k, dim, block_m, offsets.data_ptr(), sorted_token.data_ptr(), sorted_w.data_ptr(),
+           token_pos.data_ptr(), x_perm.data_ptr(), tiles.data_ptr(), tl, chunk_base.data_ptr(), _stream(x)),
+        "moe_permute",
+    )
+    return PermuteResult(offsets, sorted_token, sorted_w, token_pos, x_perm, tiles, block_m)
+
+
+def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                     n_experts: int, dim_ffn: int, block_m: int) -> torch.Tensor:
+    """h = up(x) * silu(gate(x)) over every expert's rows (mlp.py:22-23)."""
+    fn = _kernel("moe_gemm_gate_up")
+    _require_gpu(x_perm, "x_perm", 2)
+    code = _dtype_code(x_perm, "x_perm")
+    n_rows, dim = x_perm.shape
+    h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
+    _check(
+        fn(x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(), w_up.data_ptr(), code, n_rows,
+           n_experts, dim, dim_ffn, block_m, h.data_ptr(), _stream(x_perm)),
+        "moe_gemm_gate_up",
+    )
+    return h
+
+
+def _out_buffer(out: torch.Tensor | None, rows: int, cols: int, like: torch.Tensor) -> torch.Tensor:
+    if out is None:
+        return torch.empty(rows, cols, dtype=like.dtype, device=like.device)
+    _require_gpu(out, "out", 2)
+    if tuple(out.shape) != (rows, cols) or out.dtype != like.dtype or out.device != like.device:
+        raise ValueError(f"out must be [{rows}, {cols}] {like.dtype} on {like.device}")
+    return out
+
+
+def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
+                  n_experts: int, dim: int, block_m: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = down(h) * routing weight over every expert's rows (mlp.py:24, :97)."""
+    fn = _kernel("moe_gemm_down")
+    _require_gpu(h, "h", 2)
+    code = _dtype_code(h, "h")
+    n_rows, dim_ffn = h.shape
+    if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
+        raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    y = _out_buffer(out, n_rows, dim, h)
+    _check(
+        fn(h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), sorted_w.data_ptr(), code, n_rows,
+           n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
+        "moe_gemm_down",
+    )
+    return y
+
+
+def moe_combine(y: torch.Tensor, token_pos: torch.Tensor, shared: torch.Tensor | None = None) -> torch.Tensor:
+    """out = mean(shared experts) + sum over experts (ascending) of y rows
+    (mlp.py:89, :98, :77, :71)."""
+    fn = _kernel("moe_combine")
+    _require_gpu(y, "y", 2)
+    code = _dtype_code(y, "y")
+    _require_gpu(token_pos, "token_pos", 2)
+    n_tokens, top_k = token_pos.shape
+    dim = y.shape[1]
+    if y.shape[0] != n_tokens * top_k:
+        raise ValueError("y must hold n_tokens * top_k rows")
+    n_shared = 0
+    if shared is not None:
+        _require_gpu(shared, "shared", 3)
+        if shared.shape[1:] != (n_tokens, dim) or shared.dtype != y.dtype:
+            raise ValueError("shared must be [n_shared, n_tokens, dim] of y's dtype")
+        n_shared = shared.shape[0]
+    out = torch.empty(n_tokens, dim, dtype=y.dtype, device=y.device)
+    _check(
+        fn(y.data_ptr(), token_pos.data_ptr(), _ptr(shared), n_shared, code, n_tokens, top_k, dim, out.data_ptr(),
+           _stream(y)),
+        "moe_combine",
+    )
+    return out
+
+
+_dense_cache: dict[tuple, tuple[torch.Tensor, torch.Tensor]] = {}
+
+
+def _dense_tiles(n_tokens: int, block_m: int, device: torch.device, dtype: torch.dtype):
+    """Tile list and unit row weights for running one dense MLP over all
+    tokens (shared experts) through the grouped GEMMs."""
+    key = (n_tokens, block_m, device, dtype)
+    hit = _dense_cache.get(key)
+    if hit is None:
+        n = -(-n_tokens // block_m)
+        tl = [n, block_m, n, 0]
+        for i in range(n):
+            tl += [0, i * block_m, n_tokens]
+        hit = (torch.tensor(tl, dtype=torch.int32).to(device), torch.ones(n_tokens, dtype=dtype, device=device))
+        if len(_dense_cache) > 64:
+            _dense_cache.clear()
+        _dense_cache[key] = hit
+    return hit
+
+
+def moe_dense_mlp(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                  dim_ffn: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One expert ``down(up(x) * silu(gate(x)))`` over all rows of x (mlp.py:22-25),
+    on the grouped-GEMM kernels with one-entry weight tables."""
+    n_tokens, dim = x.shape
+    block_m = select_block_m(n_tokens, 1, 1, dim, dim_ffn, x.dtype)
+    tiles, ones = _dense_tiles(n_tokens, block_m, x.device, x.dtype)
+    h = moe_gemm_gate_up(x, tiles, w_gate, w_up, 1, dim_ffn, block_m)
+    return moe_gemm_down(h, tiles, w_down, ones, 1, dim, block_m, out=out)
+
+
+def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                       w_down: torch.Tensor, dim_ffn: int, top_k: int,
+                       shared: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed experts plus combine (mlp.py:84-100 and :71) for ``x [T, D]``
+    given the router logits and the experts' weight-pointer tables."""
+    n_tokens, dim = x.shape
+    n_experts = logits.shape[1]
+    if n_tokens == 0:
+        return torch.empty(0, dim, dtype=x.dtype, device=x.device)
+    block_m = select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
+    route = moe_route(logits, top_k)
+    perm = moe_permute(route, x, n_experts, block_m)
+    h = moe_gemm_gate_up(perm.x_perm, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m)
+    y = moe_gemm_down(h, perm.tiles, w_down, perm.sorted_w, n_experts, dim, block_m)
+    return moe_combine(y, perm.token_pos, shared)

@@ -1,0 +1,182 @@
+"""Drop-in MoE FFN layer running on the MI355X HIP kernels.
+
+Keeps the module contract of the reference's ``astrai/model/components/
+mlp.py``:
+
+* ``FFNFactory`` with ``"mlp"`` -> ``MLP`` and ``"moe"`` -> ``DeepSeekMoE``
+  (``mlp.py:10-28``), created through kwarg-filtering ``create``;
+* ``DeepSeekMoE(dim, dim_ffn, n_routed_experts, n_shared_experts=1,
+  n_activated_experts=2, topk_method="greedy", n_layers=1)`` with the same
+  child modules and therefore the same ``state_dict`` keys:
+  ``router.weight``, ``shared_experts.{i}.{up,gate,down}.weight``,
+  ``routed_experts.{e}.{up,gate,down}.weight`` (``mlp.py:47-62``), and the
+  same init scales;
+* ``forward(x [B, S, D]) -> [B, S, D]`` in x's dtype (``mlp.py:64-72``).
+
+The router GEMM stays ``self.router(x)`` (``F.linear``, ``mlp.py:83``), so
+the logits are the reference's by construction; everything after it — softmax,
+top-k, renormalisation, permutation, the expert SwiGLU GEMMs, the weighted
+combine and the shared-expert mean — runs in the HIP kernels of
+``astrai_amd.extension`` with the reference's rounding points.
+
+The HIP path is the only path: inputs it cannot take (CPU tensors, dtypes
+other than float32/bfloat16, autograd through the layer, experts whose
+``up/gate/down`` are not bias-free ``Linear`` modules, e.g. after LoRA
+injection) raise instead of silently running something else.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from astrai_amd.extension import ops
+from astrai_amd.factory import BaseFactory
+from astrai_amd.model.components.linear import Linear
+
+
+class FFNFactory(BaseFactory[nn.Module]):
+    pass
+
+
+def _check_gpu_input(x: Tensor, params: list[Tensor], who: str) -> None:
+    if x.device.type != "cuda":
+        raise RuntimeError(f"{who} runs on the HIP kernels and needs a ROCm device tensor, got {x.device}")
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"{who} supports float32 and bfloat16 activations, got {x.dtype}")
+    for p in params:
+        if p.device != x.device or p.dtype != x.dtype:
+            raise RuntimeError(f"{who}: parameters must be on {x.device} in {x.dtype}, found {p.device}/{p.dtype}")
+    if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in params)):
+        raise NotImplementedError(
+            f"{who} implements the forward pass only; run it under torch.no_grad() or torch.inference_mode()"
+        )
+
+
+def _plain_linear(m: nn.Module, who: str) -> Tensor:
+    if type(m) is not Linear or m.bias is not None:
+        raise RuntimeError(f"{who}: expert projections must be bias-free Linear modules, got {type(m).__name__}")
+    return m.weight
+
+
+@FFNFactory.register("mlp")
+class MLP(nn.Module):
+    """Dense SwiGLU expert ``down(up(x) * silu(gate(x)))`` (``mlp.py:14-25``)."""
+
+    def __init__(self, dim: int, dim_ffn: int, down_init_std: float = 0.02):
+        super().__init__()
+        self.up = Linear(dim, dim_ffn)
+        self.gate = Linear(dim, dim_ffn)
+        self.down = Linear(dim_ffn, dim, init_std=down_init_std)
+
+    def weights(self) -> tuple[Tensor, Tensor, Tensor]:
+        return (
+            _plain_linear(self.gate, "MLP"),
+            _plain_linear(self.up, "MLP"),
+            _plain_linear(self.down, "MLP"),
+        )
+
+    def forward(self, x: Tensor) -> Tensor:
+        wg, wu, wd = self.weights()
+        _check_gpu_input(x, [wg, wu, wd], "MLP")
+        lead, dim = x.shape[:-1], x.shape[-1]
+        x2 = x.reshape(-1, dim).contiguous()
+        tables = [ops.expert_weight_table([w], tuple(w.shape)) for w in (wg, wu, wd)]
+        out = ops.moe_dense_mlp(x2, *tables, wg.shape[0])
+        return out.view(*lead, dim)
+
+
+@FFNFactory.register("moe")
+class DeepSeekMoE(nn.Module):
+    def __init__(
+        self,
+        dim: int,
+        dim_ffn: int,
+        n_routed_experts: int,
+        n_shared_experts: int = 1,
+        n_activated_experts: int = 2,
+        topk_method: str = "greedy",
+        n_layers: int = 1,
+    ):
+        super().__init__()
+        self.dim = dim
+        self.n_routed_experts = n_routed_experts
+        self.n_shared_experts = n_shared_experts
+        self.n_activated_experts = n_activated_experts
+        self.topk_method = topk_method
+
+        self.router = Linear(dim, n_routed_experts, bias=False)
+        moe_scale = 1 / max(n_shared_experts, 1) + 1 / n_activated_experts
+        down_init_std = 0.02 / (2 * n_layers * moe_scale) ** 0.5
+        self.shared_experts = nn.ModuleList(
+            [MLP(dim, dim_ffn, down_init_std=down_init_std) for _ in range(n_shared_experts)]
+        )
+        self.routed_experts = nn.ModuleList(
+            [MLP(dim, dim_ffn, down_init_std=down_init_std) for _ in range(n_routed_experts)]
+        )
+        # Device pointer tables of the expert weights, rebuilt when any
+        # weight's storage moves (not part of the state_dict).
+        self._table_key: tuple | None = None
+        self._tables: tuple[Tensor, ...] | None = None
+
+    # -- weight-pointer tables -------------------------------------------------
+    def _expert_weights(self, experts: nn.ModuleList) -> tuple[list[Tensor], list[Tensor], list[Tensor]]:
+        g, u, d = [], [], []
+        for e in experts:
+            wg, wu, wd = e.weights()
+            g.append(wg)
+            u.append(wu)
+            d.append(wd)
+        return g, u, d
+
+    def _weight_tables(self) -> tuple[Tensor, ...]:
+        routed = self._expert_weights(self.routed_experts)
+        shared = self._expert_weights(self.shared_experts)
+        key = tuple(w.data_ptr() for ws in (*routed, *shared) for w in ws)
+        if key != self._table_key or self._tables is None:
+            shape_in = tuple(routed[0][0].shape)
+            shape_out = tuple(routed[2][0].shape)
+            t_routed = (
+                ops.expert_weight_table(routed[0], shape_in),
+                ops.expert_weight_table(routed[1], shape_in),
+                ops.expert_weight_table(routed[2], shape_out),
+            )
+            t_shared = tuple(
+                tuple(ops.expert_weight_table([w], tuple(w.shape)) for w in (shared[0][i], shared[1][i], shared[2][i]))
+                for i in range(len(shared[0]))
+            )
+            self._tables = (t_routed, t_shared)
+            self._table_key = key
+        return self._tables
+
+    # -- forward ----------------------------------------------------------------
+    def forward(self, x: Tensor) -> Tensor:
+        bsz, seq_len, dim = x.shape
+        x_flat = x.view(-1, dim)
+        params = [self.router.weight] + [p for p in self.routed_experts.parameters()] + [
+            p for p in self.shared_experts.parameters()
+        ]
+        _check_gpu_input(x_flat, params, "DeepSeekMoE")
+        shared_out = self._shared_forward(x_flat)
+        out = self._routed_forward(x_flat, shared_out)
+        return out.view(bsz, seq_len, dim)
+
+    def _shared_forward(self, x: Tensor) -> Tensor | None:
+        """Each shared expert's output stacked as ``[n_shared, T, D]``; the
+        mean (``mlp.py:77``) is taken inside the combine kernel. ``None`` for
+        ``n_shared_experts == 0`` (the reference's ``zeros_like``)."""
+        if self.n_shared_experts == 0 or x.shape[0] == 0:
+            return None
+        _, t_shared = self._weight_tables()
+        dim_ffn = self.shared_experts[0].up.weight.shape[0]
+        out = torch.empty(self.n_shared_experts, x.shape[0], x.shape[1], dtype=x.dtype, device=x.device)
+        for i, (tg, tu, td) in enumerate(t_shared):
+            ops.moe_dense_mlp(x, tg, tu, td, dim_ffn, out=out[i])
+        return out
+
+    def _routed_forward(self, x: Tensor, shared: Tensor | None = None) -> Tensor:
+        (tg, tu, td), _ = self._weight_tables()
+        logits = self.router(x)
+        dim_ffn = self.routed_experts[0].up.weight.shape[0]
+        return ops.moe_routed_forward(x, logits, tg, tu, td, dim_ffn, self.n_activated_experts, shared)

@@ -1,0 +1,221 @@
+"""MoE-layer throughput on one MI355X.
+
+A step is one ``DeepSeekMoE.forward`` (router GEMM, routing, permutation,
+grouped gate/up + SwiGLU GEMM, grouped down GEMM, combine) over one batch of
+the workload's synthetic tokens, with inputs and weights resident in HBM.
+
+Prints one JSON line:
+  value           tokens/s of the whole layer forward (timed K steps)
+  gemm_tflops     algorithmic expert-GEMM FLOPs (6*T*k*D*F) / (gate_up + down
+                  kernel time), and its fraction of the 2.5 PFLOP/s dense-bf16
+                  matrix-core peak
+  roofline        the dominant kernel (grouped gate/up GEMM): algorithmic
+                  FLOPs per launch / its average launch time, measured with
+                  HIP events on the launch stream over the instrumented pass
+  kernels_ms      average time of every stage
+  cpu_baseline    the reference path (the oracle's torch restatement of
+                  mlp.py:64-100) on the host CPU, on a bounded token sample of
+                  the same layer
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
+# (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel's reading); None until
+# measured for the workload.
+MEASURED_TRAFFIC_BYTES: dict[str, float] = {}
+
+
+def _parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", default=None, help="workload name (default: the Mixtral-shaped layer)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU work for the baseline sample")
+    return p.parse_args()
+
+
+class StageTimer:
+    """Wraps the ops entry points to record HIP events around each launch on
+    the current stream (the stream the kernels are enqueued on)."""
+
+    STAGES = ("moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_down", "moe_combine")
+
+    def __init__(self, ops):
+        self.ops = ops
+        self.orig = {}
+        self.events: dict[str, list] = {s: [] for s in self.STAGES}
+
+    def __enter__(self):
+        for name in self.STAGES:
+            fn = getattr(self.ops, name)
+            self.orig[name] = fn
+
+            def wrapped(*a, _fn=fn, _name=name, **k):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                out = _fn(*a, **k)
+                e.record()
+                self.events[_name].append((s, e))
+                return out
+
+            setattr(self.ops, name, wrapped)
+        return self
+
+    def __exit__(self, *exc):
+        for name, fn in self.orig.items():
+            setattr(self.ops, name, fn)
+
+    def avg_ms(self) -> dict[str, float]:
+        return {k: (sum(s.elapsed_time(e) for s, e in v) / len(v) if v else 0.0) for k, v in self.events.items()}
+
+
+def cpu_baseline(layer, x, w, target_s: float) -> dict:
+    """The reference path on the host CPU (bounded token sample)."""
+    from oracle import moe_ref as R
+
+    threads = torch.get_num_threads()
+    rw, rb, experts, shared = R.module_weights(layer)
+    to_cpu = lambda t: None if t is None else t.detach().cpu()  # noqa: E731
+    rw, rb = to_cpu(rw), to_cpu(rb)
+    experts = [R.ExpertWeights(to_cpu(e.gate), to_cpu(e.up), to_cpu(e.down)) for e in experts]
+    x_all = x.view(-1, w.dim)
+    n_warm = min(32, x_all.shape[0])
+    with torch.no_grad():
+        xs = x_all[:n_warm].cpu()
+        t0 = time.perf_counter()
+        R.routed_forward(xs, rw, rb, experts, w.top_k)
+        t_warm = time.perf_counter() - t0
+        per_tok = max(t_warm / n_warm, 1e-6)
+        n = int(min(x_all.shape[0], max(n_warm, target_s / per_tok)))
+        xs = x_all[:n].cpu()
+        t0 = time.perf_counter()
+        R.routed_forward(xs, rw, rb, experts, w.top_k)
+        dt = time.perf_counter() - t0
+    return {
+        "value": n / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"first {n} of {x_all.shape[0]} tokens of the same layer and inputs, reference torch path "
+                  f"(mlp.py:79-100) on CPU in {str(w.dtype).replace('torch.', '')}, {dt:.1f} s",
+    }
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(
+            "bench.py measures the single-GPU MoE layer: every expert is resident on one GPU and the path has no "
+            "collectives, so only --gpus 1 is supported.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+
+    from astrai_amd.extension import ops
+    from astrai_amd.workloads import HEADLINE, WORKLOADS, make_layer, routing_stats
+
+    name = args.workload or HEADLINE
+    w = WORKLOADS[name]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    layer, x = make_layer(w, dev)
+    T = w.n_tokens
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            layer(x)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_wall = time.perf_counter()
+        start.record()
+        for _ in range(args.steps):
+            out = layer(x)
+        end.record()
+        torch.cuda.synchronize()
+        t_wall = time.perf_counter() - t_wall
+        ms_per_step = start.elapsed_time(end) / args.steps
+
+        with StageTimer(ops) as timer:
+            for _ in range(args.steps):
+                layer(x)
+            torch.cuda.synchronize()
+        stage_ms = timer.avg_ms()
+
+        logits = layer.router(x.view(-1, w.dim))
+        counts = ops.moe_route(logits, w.top_k).chunk_hist.sum(0)
+        torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+
+    bf16 = w.dtype == torch.bfloat16
+    s = 2 if bf16 else 4
+    peak = PEAK_BF16_TFLOPS if bf16 else PEAK_FP32_TFLOPS
+    rows = T * w.top_k
+    flops_gate_up = 4.0 * rows * w.dim * w.dim_ffn
+    flops_down = 2.0 * rows * w.dim * w.dim_ffn
+    t_gu, t_dn = stage_ms["moe_gemm_gate_up"] / 1e3, stage_ms["moe_gemm_down"] / 1e3
+    gemm_tflops = (flops_gate_up + flops_down) / (t_gu + t_dn) / 1e12
+    achieved = flops_gate_up / t_gu / 1e12
+    n_active = int((counts > 0).sum().item())
+    weight_bytes = n_active * 3.0 * w.dim * w.dim_ffn * s
+    bytes_permute = T * w.dim * s + rows * w.dim * s + rows * 8
+    bytes_combine = rows * w.dim * s + T * w.dim * s + rows * (s + 8)
+    traffic = MEASURED_TRAFFIC_BYTES.get(name)
+
+    result = {
+        "metric": "MoE-layer tokens/s + grouped-GEMM TFLOP/s (% of bf16 MFMA peak), 1 GPU",
+        "value": T / (ms_per_step / 1e3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "wall_s_timed": t_wall,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if bf16 else "f32",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) expert weights, random-init)",
+        "config": {**w.describe(), "parallelism": "single GPU, all experts resident"},
+        "gemm_tflops": gemm_tflops,
+        "gemm_frac_of_peak": gemm_tflops / peak,
+        "roofline": {
+            "kernel": "gemm_mfma_kernel<gate_up>" if bf16 else "gemm_generic_kernel<gate_up>",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": achieved / peak,
+            "traffic": traffic,
+            "algorithmic_flops_per_launch": flops_gate_up,
+        },
+        "kernels_ms": stage_ms,
+        "permute_gbs": bytes_permute / (stage_ms["moe_permute"] / 1e3) / 1e9,
+        "combine_gbs": bytes_combine / (stage_ms["moe_combine"] / 1e3) / 1e9,
+        "expert_weight_stream_gbs": weight_bytes / (t_gu + t_dn) / 1e9,
+        "routing": routing_stats(counts),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(layer, x, w, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

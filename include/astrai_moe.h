@@ -1,0 +1,180 @@
+/*
+ * astrai_moe.h — C ABI of the MI355X (gfx950) MoE expert-forward library
+ * (libastrai_moe.so).
+ *
+ * The library replaces the routed-expert body of AstrAI's DeepSeekMoE layer,
+ * astrai/model/components/mlp.py:79-100, and the combine at mlp.py:71.
+ * The reference has no native code for this path: the replaced "interface" is
+ * the sequence of torch calls in mlp.py, and each entry point below names the
+ * lines it stands in for.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers (HBM) unless stated; sizes are elements.
+ *   - Row-major, contiguous tensors. Expert weights keep the reference's
+ *     nn.Linear layout [out_features, in_features] (astrai/model/components/
+ *     linear.py:12) and are passed as device arrays of per-expert pointers,
+ *     so the module's parameters are used in place.
+ *   - dtype selects the element type of every floating-point tensor of the
+ *     call: ASTRAI_MOE_F32 or ASTRAI_MOE_BF16 (bf16 stored as uint16 bits).
+ *   - Work is enqueued on `stream` (a hipStream_t); nothing synchronises the
+ *     host and nothing allocates device memory.
+ *   - Return 0 on success, a negative ASTRAI_MOE_E* code on failure;
+ *     astrai_moe_last_error() then describes the failure (per host thread).
+ *   - Entry points keep no state between calls and are re-entrant; calls on
+ *     different streams may run concurrently if their buffers are disjoint.
+ */
+#ifndef ASTRAI_MOE_H
+#define ASTRAI_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ASTRAI_MOE_ABI_VERSION 1
+
+/* Element types. */
+#define ASTRAI_MOE_F32 0
+#define ASTRAI_MOE_BF16 1
+
+/* Status codes. */
+#define ASTRAI_MOE_OK 0
+#define ASTRAI_MOE_EINVAL (-1)  /* bad argument (null pointer, size, dtype) */
+#define ASTRAI_MOE_ELAUNCH (-2) /* HIP reported an error at launch */
+
+/* Tokens per routing chunk: astrai_moe_route writes one expert histogram
+ * row per chunk of this many tokens, and astrai_moe_permute ranks tokens
+ * chunk by chunk. */
+#define ASTRAI_MOE_CHUNK_TOKENS 32
+
+/* Limits of this build. */
+#define ASTRAI_MOE_MAX_EXPERTS 1024
+#define ASTRAI_MOE_MAX_TOPK 32
+
+/* Layout of the tile list written by astrai_moe_permute and read by the two
+ * grouped GEMMs (int32):
+ *   tiles[0] = number of row tiles (device-written)
+ *   tiles[1] = block_m (rows per tile)
+ *   tiles[2] = capacity (max tiles the array holds), tiles[3] = 0
+ *   then per tile i: tiles[4+3i] = expert, tiles[5+3i] = first permuted row,
+ *                    tiles[6+3i] = end of that expert's rows (exclusive).
+ * Tiles never straddle experts, so an expert with M rows has ceil(M/block_m)
+ * tiles and an expert with no rows has none. */
+#define ASTRAI_MOE_TILE_HEADER 4
+#define ASTRAI_MOE_TILE_STRIDE 3
+
+/* ABI version of the loaded library (ASTRAI_MOE_ABI_VERSION at build time). */
+int astrai_moe_abi_version(void);
+
+/* Message for the last failed call on this host thread ("" if none). */
+const char* astrai_moe_last_error(void);
+
+/* Rows per GEMM tile that the library will use for this problem. Host-side
+ * policy only; no device work. Returns a positive value or a negative code. */
+int astrai_moe_select_block_m(int64_t n_tokens, int n_experts, int top_k,
+                              int64_t dim, int64_t dim_ffn, int dtype);
+
+/* Number of int32 elements the tile list needs (header included). */
+int64_t astrai_moe_tile_list_len(int64_t n_tokens, int n_experts, int top_k,
+                                 int block_m);
+
+/*
+ * Router softmax, top-k and renormalisation.
+ * Replaces mlp.py:84 (softmax(logits.float()).to(dtype)), mlp.py:86
+ * (torch.topk(probs, K), largest, sorted) and mlp.py:87 (w / w.sum(-1)).
+ * The router GEMM itself (mlp.py:83) stays with the caller.
+ *
+ *   logits     [n_tokens, n_experts]  dtype
+ *   topk_idx   [n_tokens, top_k]      int32, experts by descending
+ *                                     probability (ties: lower expert first)
+ *   topk_w     [n_tokens, top_k]      dtype, renormalised weights
+ *   chunk_hist [ceil(n_tokens/ASTRAI_MOE_CHUNK_TOKENS), n_experts] int32,
+ *              routed-token count of every expert within each token chunk
+ */
+int astrai_moe_route(const void* logits, int dtype, int64_t n_tokens,
+                     int n_experts, int top_k, int32_t* topk_idx,
+                     void* topk_w, int32_t* chunk_hist, void* stream);
+
+/*
+ * Token permutation by expert.
+ * Replaces mlp.py:90-95: for e = 0..E-1, (topk_idx == e).nonzero() gives the
+ * tokens routed to e in ascending order, and x[token_idx] gathers their rows.
+ * The permuted order is that concatenation: expert-major, token-ascending.
+ *
+ *   topk_idx, topk_w, chunk_hist   as written by astrai_moe_route
+ *   x              [n_tokens, dim]       dtype
+ *   expert_offsets [n_experts + 1]       int32, exclusive scan of counts
+ *   sorted_token   [n_tokens * top_k]    int32, source token of each row
+ *   sorted_w       [n_tokens * top_k]    dtype, routing weight of each row
+ *   token_pos      [n_tokens * top_k]    int32, row of (token, slot)
+ *   x_perm         [n_tokens * top_k, dim] dtype, x[sorted_token]
+ *   tiles          astrai_moe_tile_list_len(...) int32, see layout above
+ *   chunk_base     [n_chunks, n_experts] int32 scratch
+ */
+int astrai_moe_permute(const int32_t* topk_idx, const void* topk_w,
+                       const int32_t* chunk_hist, const void* x, int dtype,
+                       int64_t n_tokens, int n_experts, int top_k, int64_t dim,
+                       int block_m, int32_t* expert_offsets,
+                       int32_t* sorted_token, void* sorted_w,
+                       int32_t* token_pos, void* x_perm, int32_t* tiles,
+                       int64_t tiles_len, int32_t* chunk_base, void* stream);
+
+/*
+ * Grouped gate/up projection with fused SwiGLU.
+ * Replaces mlp.py:22-23 (up(x) * silu(gate(x))) for every expert at once,
+ * rounding to dtype where the reference does: after gate, after up, after
+ * silu and after the product.
+ *
+ *   x_perm  [n_rows, dim]           dtype (n_rows = n_tokens * top_k)
+ *   tiles   tile list from astrai_moe_permute (same block_m)
+ *   w_gate, w_up  device arrays of n_experts pointers, each [dim_ffn, dim]
+ *   h       [n_rows, dim_ffn]       dtype
+ */
+int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
+                            int64_t tiles_len, const void* const* w_gate,
+                            const void* const* w_up, int dtype, int64_t n_rows,
+                            int n_experts, int64_t dim, int64_t dim_ffn,
+                            int block_m, void* h, void* stream);
+
+/*
+ * Grouped down projection with the routing-weight multiply fused.
+ * Replaces mlp.py:24 (down(gated)) and the product at mlp.py:97-98
+ * (expert_output * weights), rounding after each as the reference does.
+ *
+ *   h         [n_rows, dim_ffn]   dtype
+ *   w_down    device array of n_experts pointers, each [dim, dim_ffn]
+ *   sorted_w  [n_rows]            dtype, from astrai_moe_permute
+ *   y         [n_rows, dim]       dtype
+ */
+int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
+                         int64_t tiles_len, const void* const* w_down,
+                         const void* sorted_w, int dtype, int64_t n_rows,
+                         int n_experts, int64_t dim_ffn, int64_t dim,
+                         int block_m, void* y, void* stream);
+
+/*
+ * Weighted un-permute and combine.
+ * Replaces mlp.py:89 and :98 (zeros, then index_add_ of every expert's
+ * weighted rows in ascending expert order, rounding after each add),
+ * mlp.py:77 (mean of the shared experts' outputs: Python sum from 0, then
+ * division by n_shared, which torch evaluates as a multiply by the float
+ * reciprocal) and mlp.py:71 (shared_out + routed_out).
+ *
+ *   y          [n_tokens * top_k, dim]  dtype, from astrai_moe_gemm_down
+ *   token_pos  [n_tokens * top_k]       int32, from astrai_moe_permute
+ *   shared     [n_shared, n_tokens, dim] dtype: each shared expert's output
+ *              (NULL when n_shared == 0: the reference's zeros_like,
+ *              mlp.py:75-76)
+ *   out        [n_tokens, dim]          dtype
+ */
+int astrai_moe_combine(const void* y, const int32_t* token_pos,
+                       const void* shared, int n_shared, int dtype,
+                       int64_t n_tokens, int top_k, int64_t dim, void* out,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ASTRAI_MOE_H */

@@ -1,0 +1,197 @@
+"""Host-side contract tests (CPU): factory, module contract, loader and the
+C ABI (symbols exported, argument validation, host policy). No device work."""
+
+from __future__ import annotations
+
+import ctypes
+import inspect
+import re
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn as nn
+
+from astrai_amd.extension import KERNEL_NAMES, is_available, loader, ops
+from astrai_amd.factory import BaseFactory
+from astrai_amd.model.components.linear import Linear
+from astrai_amd.model.components.mlp import MLP, DeepSeekMoE, FFNFactory
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "astrai_moe.h"
+
+
+# -- factory (astrai/factory.py:45-147) ---------------------------------------
+
+
+def test_factory_register_create_filters_kwargs():
+    class Base(nn.Module):
+        pass
+
+    class F(BaseFactory[Base]):
+        pass
+
+    @F.register("a")
+    class A(Base):
+        def __init__(self, dim, scale=2):
+            super().__init__()
+            self.dim, self.scale = dim, scale
+
+    obj = F.create("a", dim=3, unrelated=1, vocab_size=7)
+    assert (obj.dim, obj.scale) == (3, 2)
+    with pytest.raises(ValueError, match="already registered"):
+        F.register("a")(A)
+    with pytest.raises(ValueError, match="Unknown component"):
+        F.create("b")
+    with pytest.raises(TypeError):
+
+        @F.register("c")
+        class C:  # not a Base
+            pass
+
+    assert F.list_registered() == ["a"] and F.is_registered("a")
+
+
+def test_ffn_factory_entries():
+    assert FFNFactory.get_component_class("moe") is DeepSeekMoE
+    assert FFNFactory.get_component_class("mlp") is MLP
+
+
+# -- module contract (astrai/model/components/mlp.py:28-62) -------------------
+
+
+def test_moe_constructor_signature_matches_reference():
+    sig = inspect.signature(DeepSeekMoE.__init__)
+    params = [(p.name, p.default) for p in sig.parameters.values()][1:]
+    E = inspect.Parameter.empty
+    assert params == [
+        ("dim", E),
+        ("dim_ffn", E),
+        ("n_routed_experts", E),
+        ("n_shared_experts", 1),
+        ("n_activated_experts", 2),
+        ("topk_method", "greedy"),
+        ("n_layers", 1),
+    ]
+
+
+def test_moe_state_dict_keys_and_shapes():
+    cfg = dict(dim=16, dim_ffn=24, n_routed_experts=4, n_shared_experts=2, n_activated_experts=2,
+               topk_method="greedy", n_layers=3, vocab_size=100, hidden_size=16)
+    m = FFNFactory.create("moe", **cfg)
+    sd = m.state_dict()
+    expected = {"router.weight": (4, 16)}
+    for group, n in (("shared_experts", 2), ("routed_experts", 4)):
+        for i in range(n):
+            expected[f"{group}.{i}.up.weight"] = (24, 16)
+            expected[f"{group}.{i}.gate.weight"] = (24, 16)
+            expected[f"{group}.{i}.down.weight"] = (16, 24)
+    assert {k: tuple(v.shape) for k, v in sd.items()} == expected
+    # Same init scale as the reference: 0.02 / sqrt(2 * n_layers * moe_scale).
+    moe_scale = 1 / 2 + 1 / 2
+    assert m.routed_experts[0].down.init_std == pytest.approx(0.02 / (2 * 3 * moe_scale) ** 0.5)
+    assert m.router.bias is None and isinstance(m.router, Linear)
+    # LoRA targets the experts' Linear children by these names.
+    assert {n.rsplit(".", 1)[-1] for n, mod in m.named_modules() if isinstance(mod, Linear)} == {
+        "router", "up", "gate", "down"}
+
+
+def test_state_dict_round_trip():
+    a = DeepSeekMoE(8, 16, 3, n_shared_experts=1)
+    for p in a.parameters():
+        nn.init.normal_(p)
+    b = DeepSeekMoE(8, 16, 3, n_shared_experts=1)
+    b.load_state_dict(a.state_dict())
+    for (ka, va), (kb, vb) in zip(a.state_dict().items(), b.state_dict().items()):
+        assert ka == kb and torch.equal(va, vb)
+
+
+def test_cpu_input_raises_instead_of_falling_back():
+    m = DeepSeekMoE(8, 16, 4, n_shared_experts=0)
+    with torch.no_grad(), pytest.raises(RuntimeError, match="ROCm device"):
+        m(torch.zeros(1, 2, 8))
+
+
+# -- loader (astrai/extension/loader.py:14-36) --------------------------------
+
+
+def test_loader_contract():
+    assert KERNEL_NAMES == ["moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_down", "moe_combine"]
+    assert loader.load_error() is None, loader.load_error()
+    for name in KERNEL_NAMES:
+        assert is_available(name)
+        assert callable(getattr(loader.get_module(name), name))
+    assert not is_available("attn_decode")
+    assert loader.get_module("nope") is None
+
+
+def test_single_hip_runtime_mapped():
+    assert len(loader._hip_runtimes_mapped()) <= 1
+
+
+def _declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(astrai_moe_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = _declared_symbols()
+    assert len(syms) >= 9, syms
+    lib = ctypes.CDLL(str(loader.LIB_PATH))
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in astrai_moe.h but not exported"
+    # ... and the loader binds every declared symbol with a signature.
+    assert set(syms) == set(loader._SIGNATURES)
+
+
+# -- C ABI host behaviour (validation happens before any device work) ---------
+
+
+def test_abi_rejects_bad_arguments_with_message():
+    lib = loader.library()
+    rc = lib.astrai_moe_route(None, 1, 10, 0, 1, None, None, None, None)
+    assert rc == -1 and "n_experts" in loader.last_error()
+    rc = lib.astrai_moe_route(None, 1, 10, 8, 9, None, None, None, None)
+    assert rc == -1 and "top_k" in loader.last_error()
+    rc = lib.astrai_moe_route(1, 7, 10, 8, 2, 1, 1, 1, None)
+    assert rc == -1 and "dtype" in loader.last_error()
+    rc = lib.astrai_moe_permute(None, None, None, None, 1, 10, 8, 2, 16, 64, None, None, None, None, None,
+                                None, 3, None, None)
+    assert rc == -1 and "tile list" in loader.last_error()
+    rc = lib.astrai_moe_combine(1, 1, None, 2, 1, 4, 2, 8, 1, None)
+    assert rc == -1 and "n_shared" in loader.last_error()
+    # Empty inputs are a valid no-op.
+    assert lib.astrai_moe_route(None, 1, 0, 8, 2, None, None, None, None) == 0
+    assert lib.astrai_moe_combine(None, None, None, 0, 1, 0, 2, 8, None, None) == 0
+
+
+def test_tile_list_len_bounds_the_tile_count():
+    """capacity >= sum_e ceil(M_e / block_m) for any split of T*K rows."""
+    import random
+
+    rnd = random.Random(0)
+    for _ in range(200):
+        n_exp = rnd.randint(1, 64)
+        k = rnd.randint(1, min(8, n_exp))
+        n_tok = rnd.randint(0, 5000)
+        bm = rnd.choice([32, 64, 256])
+        rows = n_tok * k
+        cuts = sorted(rnd.randint(0, rows) for _ in range(n_exp - 1))
+        counts = [b - a for a, b in zip([0] + cuts, cuts + [rows])]
+        need = sum(-(-c // bm) for c in counts)
+        cap = (ops.tile_list_len(n_tok, n_exp, k, bm) - ops.TILE_HEADER) // ops.TILE_STRIDE
+        assert cap >= need
+
+
+def test_block_m_policy():
+    bf = torch.bfloat16
+    assert ops.select_block_m(16384, 8, 2, 4096, 14336, bf) == 256
+    assert ops.select_block_m(64, 128, 8, 4096, 1536, bf) == 32
+    assert ops.select_block_m(1024, 8, 2, 512, 1024, torch.float32) == 64
+    assert ops.select_block_m(100, 4, 2, 8, 16, bf) == 64  # shapes the MFMA kernels do not tile
+
+
+def test_ops_validate_before_launch():
+    with pytest.raises(ValueError, match="ROCm device"):
+        ops.moe_route(torch.zeros(4, 8), 2)
+    with pytest.raises(ValueError):
+        ops.expert_weight_table([], (2, 2))

@@ -1,0 +1,323 @@
+"""Pins of the oracle (oracle/moe_ref.py) — CPU only.
+
+The reference ships no golden vectors, known-answer tests or fixtures for the
+MoE path (its only MoE test checks shape and finiteness on unseeded input), so
+the oracle is pinned here by what the mathematics fixes:
+
+  * fp64 brute force of the whole layer (per-token loop, sorted top-k);
+  * closed forms: one expert with K = 1 is the dense SwiGLU; one-hot routing
+    selects exactly one expert; uniform routing with K = E is the mean of the
+    experts; K = 1 renormalised weights are exactly 1;
+  * the permutation against a brute-force stable sort;
+  * a numpy emulation of the reference's bf16 rounding points (fp64 GEMMs,
+    bf16 rounding after every op the reference rounds after);
+  * planted mistakes: variants of the oracle with a swapped operand, a dropped
+    term, a wrong sign or order must each fail at least one of the checks
+    above, which shows the checks can see such mistakes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import moe_ref as R
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """Round float64 values to the nearest bfloat16 (ties to even), via fp32."""
+    f = np.asarray(a, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def np_silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def make_case(seed, n_tok, dim, dim_ffn, n_exp, top_k, dtype, router_std=1.0, n_shared=0, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n_tok, dim, generator=g)
+    rw = torch.randn(n_exp, dim, generator=g) * router_std
+    rb = torch.randn(n_exp, generator=g) if bias else None
+
+    def ew():
+        return R.ExpertWeights(
+            (torch.randn(dim_ffn, dim, generator=g) * 0.2).to(dtype),
+            (torch.randn(dim_ffn, dim, generator=g) * 0.2).to(dtype),
+            (torch.randn(dim, dim_ffn, generator=g) * 0.2).to(dtype),
+        )
+
+    experts = [ew() for _ in range(n_exp)]
+    shared = [ew() for _ in range(n_shared)]
+    return (x.to(dtype), rw.to(dtype), None if rb is None else rb.to(dtype), experts, shared)
+
+
+def brute_fp64(x, rw, rb, experts, shared, top_k):
+    """Whole layer in float64, one token at a time (mlp.py semantics without
+    rounding); top-k by a stable descending sort."""
+    X = x.double().numpy()
+    logits = X @ rw.double().numpy().T
+    if rb is not None:
+        logits = logits + rb.double().numpy()
+    out = np.zeros_like(X)
+    mlps = [(w.gate.double().numpy(), w.up.double().numpy(), w.down.double().numpy()) for w in experts]
+    for t in range(X.shape[0]):
+        z = logits[t] - logits[t].max()
+        p = np.exp(z) / np.exp(z).sum()
+        order = sorted(range(len(p)), key=lambda i: (-p[i], i))[:top_k]
+        w = p[order] / p[order].sum()
+        for wi, e in zip(w, order):
+            g, u, d = mlps[e]
+            out[t] += wi * (((X[t] @ u.T) * np_silu(X[t] @ g.T)) @ d.T)
+    if shared:
+        acc = np.zeros_like(X)
+        for s in shared:
+            g, u, d = (s.gate.double().numpy(), s.up.double().numpy(), s.down.double().numpy())
+            acc += ((X @ u.T) * np_silu(X @ g.T)) @ d.T
+        out += acc / len(shared)
+    return out
+
+
+def emulate_bf16(x, rw, experts, top_k):
+    """The reference's bf16 routed forward with every rounding point made
+    explicit: fp64 products, bf16 rounding where the reference's tensors are
+    bf16. Requires tie-free routing (top-k ties are resolved differently by
+    different top-k implementations)."""
+    X = x.double().numpy()
+    logits = bf16_round(X @ rw.double().numpy().T)
+    z = logits - logits.max(-1, keepdims=True)
+    p = bf16_round((np.exp(z) / np.exp(z).sum(-1, keepdims=True)).astype(np.float32))
+    n_tok, dim = X.shape
+    out = np.zeros((n_tok, dim))
+    order = np.argsort(-p, axis=-1, kind="stable")[:, :top_k]
+    vals = np.take_along_axis(p, order, -1)
+    wsum = bf16_round(vals.astype(np.float32).sum(-1, keepdims=True))
+    wts = bf16_round((vals.astype(np.float32) / wsum.astype(np.float32)))
+    for e, w in enumerate(experts):
+        tok, slot = np.nonzero(order == e)
+        if tok.size == 0:
+            continue
+        xe = X[tok]
+        g = bf16_round(xe @ w.gate.double().numpy().T)
+        u = bf16_round(xe @ w.up.double().numpy().T)
+        s = bf16_round(np_silu(g.astype(np.float32)).astype(np.float32))
+        h = bf16_round(u * s)
+        y = bf16_round(h @ w.down.double().numpy().T)
+        yw = bf16_round(y * wts[tok, slot][:, None])
+        out[tok] = bf16_round(out[tok] + yw)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the pin checks, parameterised by the oracle module so planted mistakes can
+# be run through the same checks
+# ---------------------------------------------------------------------------
+
+
+def _call(fn):
+    try:
+        return bool(fn())
+    except Exception:
+        return False
+
+
+def pin_fp64_fp32(R):
+    for seed in range(3):
+        x, rw, rb, experts, shared = make_case(seed, 24, 16, 16, 5, 2, torch.float32, router_std=2.0, n_shared=1,
+                                               bias=True)
+        got = R.moe_forward(x.view(2, 12, 16), rw, rb, experts, shared, 2).view(24, 16).double().numpy()
+        ref = brute_fp64(x, rw, rb, experts, shared, 2)
+        if not np.allclose(got, ref, rtol=1e-5, atol=1e-6):
+            return False
+    return True
+
+
+def pin_fp64_bf16(R):
+    for seed in range(3):
+        x, rw, rb, experts, shared = make_case(10 + seed, 32, 32, 48, 6, 3, torch.bfloat16, router_std=2.0)
+        got = R.routed_forward(x, rw, rb, experts, 3).double().numpy()
+        ref = brute_fp64(x.float(), rw.float(), None, experts, [], 3)
+        scale = np.abs(ref).max()
+        if np.abs(got - ref).max() > 0.03 * scale:
+            return False
+    return True
+
+
+def pin_single_expert(R):
+    for dtype in (torch.float32, torch.bfloat16):
+        x, rw, rb, experts, _ = make_case(3, 16, 16, 24, 1, 1, dtype)
+        routed = R.routed_forward(x, rw, None, experts, 1)
+        dense = R.expert_mlp(x, experts[0])
+        if not torch.equal(routed, dense):
+            return False
+        w = experts[0]
+        textbook = (x.double() @ w.up.double().T) * F.silu(x.double() @ w.gate.double().T) @ w.down.double().T
+        tol = 1e-5 if dtype == torch.float32 else 3e-2
+        if (dense.double() - textbook).abs().max() > tol * textbook.abs().max():
+            return False
+    return True
+
+
+def pin_one_hot(R):
+    x, rw, _, experts, _ = make_case(4, 20, 16, 16, 4, 1, torch.float32)
+    rw = torch.zeros_like(rw)
+    rb = torch.tensor([0.0, 0.0, 60.0, 0.0])
+    out = R.routed_forward(x, rw, rb, experts, 1)
+    return torch.equal(out, R.expert_mlp(x, experts[2]))
+
+
+def pin_uniform_mean(R):
+    x, rw, _, experts, _ = make_case(5, 12, 16, 16, 4, 4, torch.float32)
+    out = R.routed_forward(x, torch.zeros_like(rw), None, experts, 4).double()
+    mean = sum(R.expert_mlp(x.double(), R.ExpertWeights(w.gate.double(), w.up.double(), w.down.double()))
+               for w in experts) / 4
+    return torch.allclose(out, mean, rtol=1e-5, atol=1e-6)
+
+
+def pin_k1_weights(R):
+    x, rw, _, _, _ = make_case(6, 64, 16, 16, 8, 1, torch.bfloat16)
+    w, _ = R.route(F.linear(x, rw), 1, torch.bfloat16)
+    return bool((w == 1).all())
+
+
+def pin_permutation(R):
+    g = torch.Generator().manual_seed(7)
+    n_tok, n_exp, k = 50, 9, 3
+    idx = torch.stack([torch.randperm(n_exp, generator=g)[:k] for _ in range(n_tok)])
+    toks, slots, offsets = R.permutation(idx, n_exp)
+    pairs = sorted(((int(idx[t, s]), t, s) for t in range(n_tok) for s in range(k)))
+    ok = toks.tolist() == [p[1] for p in pairs] and slots.tolist() == [p[2] for p in pairs]
+    counts = np.bincount(idx.flatten().numpy(), minlength=n_exp)
+    return ok and offsets.tolist() == [0] + np.cumsum(counts).tolist()
+
+
+def pin_rounding_points(R):
+    """Bitwise agreement with the rounding-point emulation on >= 99% of
+    outputs (the rest: fp32-vs-fp64 accumulation flips of a bf16 rounding)."""
+    agree = []
+    for seed in range(2):
+        x, rw, _, experts, _ = make_case(20 + seed, 64, 64, 96, 4, 2, torch.bfloat16, router_std=1.0)
+        got = R.routed_forward(x, rw, None, experts, 2).double().numpy()
+        ref = emulate_bf16(x, rw, experts, 2)
+        agree.append(np.mean(got == ref))
+    return min(agree) >= 0.99
+
+
+PINS = {
+    "fp64_fp32": pin_fp64_fp32,
+    "fp64_bf16": pin_fp64_bf16,
+    "single_expert": pin_single_expert,
+    "one_hot": pin_one_hot,
+    "uniform_mean": pin_uniform_mean,
+    "k1_weights": pin_k1_weights,
+    "permutation": pin_permutation,
+    "rounding_points": pin_rounding_points,
+}
+
+
+def run_pins(R):
+    return {name: _call(lambda f=f: f(R)) for name, f in PINS.items()}
+
+
+@pytest.mark.parametrize("name", sorted(PINS))
+def test_oracle_pin(name):
+    assert _call(lambda: PINS[name](R)), f"oracle fails pin {name}"
+
+
+# ---------------------------------------------------------------------------
+# planted mistakes (in the oracle, on the CPU): every one must be rejected
+# ---------------------------------------------------------------------------
+
+
+def _swap_gate_up(x, w):
+    return F.linear(F.linear(x, w.gate) * F.silu(F.linear(x, w.up)), w.down)
+
+
+def _silu_sign(x, w):
+    return F.linear(F.linear(x, w.up) * F.silu(-F.linear(x, w.gate)), w.down)
+
+
+def _no_silu_round(x, w):
+    g = F.linear(x, w.gate).float()
+    return F.linear((F.linear(x, w.up).float() * F.silu(g)).to(x.dtype), w.down)
+
+
+def _down_transposed(x, w):
+    return F.linear(F.linear(x, w.up) * F.silu(F.linear(x, w.gate)), w.down.t())
+
+
+def _no_renorm(logits, top_k, dtype):
+    probs = torch.softmax(logits.float(), dim=-1).to(dtype)
+    return torch.topk(probs, top_k, dim=-1)
+
+
+def _smallest(logits, top_k, dtype):
+    probs = torch.softmax(logits.float(), dim=-1).to(dtype)
+    w, i = torch.topk(probs, top_k, dim=-1, largest=False)
+    return w / w.sum(-1, keepdim=True), i
+
+
+def _renorm_sum_unrounded(logits, top_k, dtype):
+    probs = torch.softmax(logits.float(), dim=-1).to(dtype)
+    w, i = torch.topk(probs, top_k, dim=-1)
+    return (w.float() / w.float().sum(-1, keepdim=True)).to(dtype), i
+
+
+def _perm_descending(topk_idx, n_experts):
+    toks, slots, offs = R.__dict__["_orig_permutation"](topk_idx, n_experts)
+    return toks.flip(0), slots.flip(0), offs
+
+
+MUTANTS = {
+    "swap_gate_up": ("expert_mlp", _swap_gate_up),
+    "silu_sign": ("expert_mlp", _silu_sign),
+    "silu_not_rounded": ("expert_mlp", _no_silu_round),
+    "down_transposed": ("expert_mlp", _down_transposed),
+    "no_renorm": ("route", _no_renorm),
+    "topk_smallest": ("route", _smallest),
+    "renorm_sum_unrounded": ("route", _renorm_sum_unrounded),
+    "perm_descending": ("permutation", _perm_descending),
+}
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_planted_mistake_is_caught(mutant, monkeypatch):
+    attr, bad = MUTANTS[mutant]
+    monkeypatch.setitem(R.__dict__, "_orig_permutation", R.permutation)
+    monkeypatch.setattr(R, attr, bad)
+    result = run_pins(R)
+    assert not all(result.values()), f"planted mistake {mutant} passed every pin: {result}"
+
+
+def test_combine_order_mistake_is_caught(monkeypatch):
+    """Accumulating the experts' rows in descending expert order (a changed
+    rounding order) must break the rounding-point pin."""
+    orig = R.routed_forward
+
+    def descending(x, rw, rb, experts, top_k, trace=False):
+        logits = F.linear(x, rw, rb)
+        w, idx = R.route(logits, top_k, x.dtype)
+        out = torch.zeros_like(x)
+        for e in reversed(range(len(experts))):
+            tok, slot = (idx == e).nonzero(as_tuple=True)
+            if tok.numel():
+                out.index_add_(0, tok, R.expert_mlp(x[tok], experts[e]) * w[tok, slot].unsqueeze(-1))
+        return out
+
+    monkeypatch.setattr(R, "routed_forward", descending)
+    # K = 2 sums are order-free (a + b == b + a); use K = 3 to expose order.
+    x, rw, _, experts, _ = make_case(30, 64, 64, 96, 4, 3, torch.bfloat16)
+    got = R.routed_forward(x, rw, None, experts, 3).double().numpy()
+    ref = emulate_bf16(x, rw, experts, 3)
+    assert np.mean(got == ref) < 0.99
+    monkeypatch.setattr(R, "routed_forward", orig)
+    got = R.routed_forward(x, rw, None, experts, 3).double().numpy()
+    assert np.mean(got == ref) >= 0.99
