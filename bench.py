@@ -46,6 +46,9 @@ def _parse():
     p.add_argument("--workload", default=None, help="workload name (default: the Mixtral-shaped layer)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU work for the baseline sample")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="before timing, copy a buffer of this many MiB once (a plain copy kernel of known size "
+                        "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     return p.parse_args()
 
 
@@ -96,11 +99,15 @@ def cpu_baseline(layer, x, w, target_s: float) -> dict:
     x_all = x.view(-1, w.dim)
     n_warm = min(32, x_all.shape[0])
     with torch.no_grad():
-        xs = x_all[:n_warm].cpu()
-        t0 = time.perf_counter()
-        R.routed_forward(xs, rw, rb, experts, w.top_k)
-        t_warm = time.perf_counter() - t0
-        per_tok = max(t_warm / n_warm, 1e-6)
+        # warm-up, then a calibration sample sized from it, then the timed
+        # sample sized to about target_s seconds of CPU work
+        n = n_warm
+        for _ in range(2):
+            xs = x_all[:n].cpu()
+            t0 = time.perf_counter()
+            R.routed_forward(xs, rw, rb, experts, w.top_k)
+            per_tok = max((time.perf_counter() - t0) / n, 1e-7)
+            n = int(min(x_all.shape[0], max(n_warm, 0.2 * target_s / per_tok)))
         n = int(min(x_all.shape[0], max(n_warm, target_s / per_tok)))
         xs = x_all[:n].cpu()
         t0 = time.perf_counter()
@@ -138,6 +145,12 @@ def main():
     torch.cuda.set_device(dev)
     layer, x = make_layer(w, dev)
     T = w.n_tokens
+    if args.copy_probe_mib:
+        src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     with torch.inference_mode():
         for _ in range(args.warmup):
