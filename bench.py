@@ -32,10 +32,15 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc
-# (FETCH_SIZE + WRITE_SIZE, scaled by a copy kernel's reading); None until
-# measured for the workload.
-MEASURED_TRAFFIC_BYTES: dict[str, float] = {}
+# Bytes moved between L2 and memory per launch of the dominant kernel (the
+# grouped gate/up GEMM), measured with rocprofv3 --pmc: FETCH_SIZE x 2 +
+# WRITE_SIZE (KiB). A 1 GiB device copy in the same run reads back as
+# FETCH_SIZE = 0.5 GiB and WRITE_SIZE = 1 GiB, so FETCH_SIZE is scaled by 2
+# (it counts this part's 128-byte read requests as 64 bytes). Source:
+# profiles/moe_layer_d4096_f14336_e8_k2_t16384.md.
+MEASURED_TRAFFIC_BYTES: dict[str, float] = {
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (6643414.5 * 2 + 917504.0) * 1024,
+}
 
 
 def _parse():

@@ -130,9 +130,9 @@ def _call(fn):
 
 
 def pin_fp64_fp32(R):
-    for seed in range(3):
-        x, rw, rb, experts, shared = make_case(seed, 24, 16, 16, 5, 2, torch.float32, router_std=2.0, n_shared=1,
-                                               bias=True)
+    for seed, n_shared in ((0, 1), (1, 3), (2, 0)):
+        x, rw, rb, experts, shared = make_case(seed, 24, 16, 16, 5, 2, torch.float32, router_std=2.0,
+                                               n_shared=n_shared, bias=True)
         got = R.moe_forward(x.view(2, 12, 16), rw, rb, experts, shared, 2).view(24, 16).double().numpy()
         ref = brute_fp64(x, rw, rb, experts, shared, 2)
         if not np.allclose(got, ref, rtol=1e-5, atol=1e-6):
