@@ -53,7 +53,7 @@ extern "C" int astrai_moe_select_block_m(int64_t n_tokens, int n_experts,
     return fail(ASTRAI_MOE_EINVAL, "select_block_m: unsupported dtype %d", dtype);
   const bool mfma_shapes = dtype == ASTRAI_MOE_BF16 && dim % 64 == 0 &&
                            dim_ffn % 128 == 0 && dim % 256 == 0 &&
-                           dim < (1ll << 30) && dim_ffn < (1ll << 30);
+                           dim <= (1ll << 22) && dim_ffn <= (1ll << 22);
   if (!mfma_shapes) return 64;
   const int64_t rows_per_expert = n_tokens * top_k / n_experts;
   return rows_per_expert >= 128 ? kMfmaBigBM : kMfmaSmallBM;

@@ -53,9 +53,10 @@ constexpr int kBK = 64;             // K elements per stage
 constexpr int kRowBytes = kBK * 2;  // 128 bytes per staged row
 constexpr int kXcds = 8;
 
-template <int BM_, int BN_, int STAGES_, int WGM_, int WGN_, int GM_>
+template <int BM_, int BN_, int STAGES_, int WGM_, int WGN_, int GM_, int DMAW_>
 struct TileCfg {
   static constexpr int BM = BM_, BN = BN_, STAGES = STAGES_, WGM = WGM_, WGN = WGN_, GM = GM_;
+  static constexpr int DMAW = DMAW_;  // waves [0, DMAW) issue the LDS DMA
   static constexpr int WAVES = WGM * WGN;
   static constexpr int THREADS = WAVES * 64;
   static constexpr int WM = BM / WGM;  // rows per wave
@@ -66,10 +67,11 @@ struct TileCfg {
   static constexpr int A_BYTES = BM * kRowBytes;
   static constexpr int B_BYTES = BN * kRowBytes;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  static constexpr int A_PER_WAVE = A_BYTES / 1024 / WAVES;  // 1 KB DMA ops
-  static constexpr int B_PER_WAVE = B_BYTES / 1024 / WAVES;
+  static constexpr int A_PER_WAVE = A_BYTES / 1024 / DMAW;  // 1 KB DMA ops per issuing wave
+  static constexpr int B_PER_WAVE = B_BYTES / 1024 / DMAW;
   static constexpr int DMA_PER_WAVE = A_PER_WAVE + B_PER_WAVE;
-  static_assert(A_BYTES % (1024 * WAVES) == 0 && B_BYTES % (1024 * WAVES) == 0, "DMA ops split over waves");
+  static_assert(DMAW >= 1 && DMAW <= WAVES, "DMA waves");
+  static_assert(A_BYTES % (1024 * DMAW) == 0 && B_BYTES % (1024 * DMAW) == 0, "DMA ops split over waves");
   static_assert(WM % 32 == 0 && WN % 64 == 0, "32x32 MFMA tiles; gate/up halves");
   static_assert(STAGES >= 2 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS");
   static_assert(DMA_PER_WAVE * (STAGES - 1) <= 63, "vmcnt range");
@@ -136,42 +138,48 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   const int wm = wave / Cfg::WGN;
   const int wn = wave % Cfg::WGN;
 
-  // ---- LDS DMA sources: lane -> (row in its 8-row group, physical chunk);
-  // it fetches the logical chunk stored at that physical chunk ----
+  // ---- LDS DMA sources ----
+  // Waves [0, DMAW) issue all DMA ops (DMAW = 4 of 8 waves puts one issuing
+  // wave on each SIMD: an LDS-DMA op holds its wave until the CU's vector
+  // memory path accepts it, and meanwhile the SIMD's other wave keeps the
+  // matrix core busy). Lane -> (row in its 8-row group, physical chunk); it
+  // fetches the logical chunk stored at that physical chunk. Sources are
+  // 32-bit byte offsets from uniform tile bases.
   const int dma_row = lane >> 3;
-  const char* a_src[Cfg::A_PER_WAVE];
+  const int dw = wave < Cfg::DMAW ? wave : 0;
+  const char* a_base = reinterpret_cast<const char*>(A + (int64_t)row0 * K);
+  const char* b_base0 = reinterpret_cast<const char*>(
+      static_cast<const bf16_t*>(W0[e]) + (int64_t)nt * (kGateUp ? BN / 2 : BN) * K);
+  const char* b_base1 =
+      kGateUp ? reinterpret_cast<const char*>(static_cast<const bf16_t*>(W1[e]) + (int64_t)nt * (BN / 2) * K)
+              : b_base0;
+  uint32_t a_src[Cfg::A_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < Cfg::A_PER_WAVE; ++i) {
-    const int r = (wave * Cfg::A_PER_WAVE + i) * 8 + dma_row;
-    const int gr = row0 + min(r, rows - 1);  // pad rows re-read a valid row
-    a_src[i] = reinterpret_cast<const char*>(A + (int64_t)gr * K) + (((lane & 7) ^ Cfg::swz(r)) << 4);
-  }
-  const char* b_src[Cfg::B_PER_WAVE];
-  const bf16_t* B0 = static_cast<const bf16_t*>(W0[e]);
-  const bf16_t* B1 = kGateUp ? static_cast<const bf16_t*>(W1[e]) : nullptr;
+    const int r = (dw * Cfg::A_PER_WAVE + i) * 8 + dma_row;
+    a_src[i] = (uint32_t)min(r, rows - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ Cfg::swz(r)) << 4);
+  }  // pad rows re-read a valid row
+  uint32_t b_src[Cfg::B_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
-    const int r = (wave * Cfg::B_PER_WAVE + i) * 8 + dma_row;
-    const bf16_t* base;
-    int n;
-    if (kGateUp) {
-      const bool up = r >= BN / 2;
-      base = up ? B1 : B0;
-      n = nt * (BN / 2) + (up ? r - BN / 2 : r);
-    } else {
-      base = B0;
-      n = nt * BN + r;
-    }
-    b_src[i] = reinterpret_cast<const char*>(base + (int64_t)n * K) + (((lane & 7) ^ Cfg::swz(r)) << 4);
+    const int r = (dw * Cfg::B_PER_WAVE + i) * 8 + dma_row;
+    const int rr = (kGateUp && r >= BN / 2) ? r - BN / 2 : r;  // up rows follow the gate rows
+    b_src[i] = (uint32_t)rr * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ Cfg::swz(r)) << 4);
   }
   auto issue_stage = [&](int kstep, int buf) {
+    if (wave >= Cfg::DMAW) return;
     char* sa = smem + buf * Cfg::STAGE_BYTES;
     char* sb = sa + Cfg::A_BYTES;
-    const int koff = kstep * kRowBytes;
+    const uint32_t koff = kstep * kRowBytes;
 #pragma unroll
-    for (int i = 0; i < Cfg::A_PER_WAVE; ++i) lds_dma_16(a_src[i] + koff, sa + (wave * Cfg::A_PER_WAVE + i) * 1024);
+    for (int i = 0; i < Cfg::A_PER_WAVE; ++i)
+      lds_dma_16(a_base + (a_src[i] + koff), sa + (wave * Cfg::A_PER_WAVE + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < Cfg::B_PER_WAVE; ++i) lds_dma_16(b_src[i] + koff, sb + (wave * Cfg::B_PER_WAVE + i) * 1024);
+    for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
+      const int r0 = (wave * Cfg::B_PER_WAVE + i) * 8;  // uniform
+      const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
+      lds_dma_16(bb + (b_src[i] + koff), sb + (wave * Cfg::B_PER_WAVE + i) * 1024);
+    }
   };
 
   // ---- MFMA fragment reads ----
@@ -314,11 +322,12 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   }
 }
 
-// Prefill tiles: 256 x 256 outputs, 8 waves (2 per SIMD) of 128 x 64 each.
-using BigCfg = TileCfg<kMfmaBigBM, 256, 2, 2, 4, 8>;
+// Prefill tiles: 256 x 256 outputs, 8 waves (2 per SIMD) of 128 x 64 each;
+// waves 0-3 (one per SIMD) issue the DMA.
+using BigCfg = TileCfg<kMfmaBigBM, 256, 2, 2, 4, 8, 4>;
 // Decode tiles: 32 x 256 outputs, 4 waves of 32 x 64, four stages in flight
-// to keep the expert-weight stream busy.
-using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8>;
+// to keep the expert-weight stream busy; every wave issues DMA.
+using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8, 4>;
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
@@ -339,13 +348,14 @@ int launch(const void* A, const int32_t* tiles, int64_t capacity, const void* co
 }  // namespace
 
 bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m, const void* a, const void* c) {
+  // 32-bit DMA offsets: a tile spans at most 256 rows of K * 2 bytes
   return (block_m == kMfmaBigBM || block_m == kMfmaSmallBM) && dim % kBK == 0 && dim_ffn % 128 == 0 &&
-         dim < (1ll << 30) && dim_ffn < (1ll << 30) && aligned16(a) && aligned16(c);
+         dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m, const void* a, const void* c) {
   return (block_m == kMfmaBigBM || block_m == kMfmaSmallBM) && dim_ffn % kBK == 0 && dim % 256 == 0 &&
-         dim < (1ll << 30) && dim_ffn < (1ll << 30) && aligned16(a) && aligned16(c);
+         dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
