@@ -16,22 +16,29 @@
 // rounding after every add, then added to the shared output. Results are
 // bit-identical to the reference's sequence of bf16/fp32 adds.
 //
-// One wave per token; lanes stream the row with 16-byte vectors.
+// One wave per (token, column segment); lanes stream the segment with 16-byte
+// vectors. Rows are split into segments only when there are too few tokens to
+// keep the GPU busy (decode); otherwise a wave takes the whole row.
 #include "moe_common.h"
 
 namespace astrai_moe {
 namespace {
 
 constexpr int kCombineThreads = 256;
-constexpr int kTokensPerBlock = kCombineThreads / 64;
+constexpr int kWavesPerBlock = kCombineThreads / 64;
+constexpr int64_t kTargetWaves = 4096;
 
 template <typename T, int VW>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
     const T* __restrict__ y, const int32_t* __restrict__ token_pos,
     const T* __restrict__ shared, int n_shared, float inv_shared,
-    int64_t n_tokens, int top_k, int64_t dim, T* __restrict__ out) {
+    int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, T* __restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * kTokensPerBlock + (threadIdx.x >> 6);
+  const int64_t nvec = dim / VW;
+  const int64_t nseg = (nvec + seg_units - 1) / seg_units;
+  const int64_t gw = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t t = gw / nseg;
+  const int64_t seg = gw - t * nseg;
   if (t >= n_tokens) return;
 
   // Lane k < top_k holds row k; rank rows by position (distinct values, an
@@ -54,8 +61,8 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
     }
   }
 
-  const int64_t nvec = dim / VW;
-  for (int64_t v = lane; v < nvec; v += 64) {
+  const int64_t v_end = min(nvec, (seg + 1) * seg_units);
+  for (int64_t v = seg * seg_units + lane; v < v_end; v += 64) {
     float acc[VW];
 #pragma unroll
     for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
@@ -102,21 +109,29 @@ int launch_combine(const void* y, const int32_t* token_pos, const void* shared,
                    int n_shared, int64_t n_tokens, int top_k, int64_t dim,
                    void* out, hipStream_t s) {
   const float inv_shared = n_shared > 0 ? 1.0f / (float)n_shared : 0.0f;
-  const unsigned grid = (unsigned)ceil_div(n_tokens, kTokensPerBlock);
   constexpr int kVW = 16 / sizeof(T);
   const bool vec = dim % kVW == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
                    (!shared || reinterpret_cast<uintptr_t>(shared) % 16 == 0);
+  const int64_t nvec = vec ? dim / kVW : dim;
+  // segments of >= 128 units, as many as needed to reach kTargetWaves waves
+  int64_t nseg = ceil_div(kTargetWaves, n_tokens);
+  if (nseg > nvec / 128) nseg = nvec / 128;
+  if (nseg < 1) nseg = 1;
+  const int64_t seg_units = ceil_div(nvec, nseg);
+  const int64_t waves = n_tokens * ceil_div(nvec, seg_units);
+  const int64_t grid = ceil_div(waves, kWavesPerBlock);
+  if (grid >= (1ll << 31)) return fail(ASTRAI_MOE_EINVAL, "combine: too many tokens");
   if (vec)
-    hipLaunchKernelGGL((combine_kernel<T, kVW>), dim3(grid), dim3(kCombineThreads),
+    hipLaunchKernelGGL((combine_kernel<T, kVW>), dim3((unsigned)grid), dim3(kCombineThreads),
                        0, s, static_cast<const T*>(y), token_pos,
                        static_cast<const T*>(shared), n_shared, inv_shared,
-                       n_tokens, top_k, dim, static_cast<T*>(out));
+                       n_tokens, top_k, dim, seg_units, static_cast<T*>(out));
   else
-    hipLaunchKernelGGL((combine_kernel<T, 1>), dim3(grid), dim3(kCombineThreads),
+    hipLaunchKernelGGL((combine_kernel<T, 1>), dim3((unsigned)grid), dim3(kCombineThreads),
                        0, s, static_cast<const T*>(y), token_pos,
                        static_cast<const T*>(shared), n_shared, inv_shared,
-                       n_tokens, top_k, dim, static_cast<T*>(out));
+                       n_tokens, top_k, dim, seg_units, static_cast<T*>(out));
   return check_launch("combine_kernel");
 }
 

@@ -14,13 +14,16 @@
 //                   expert's segment; the GEMM row-tile list is laid out from
 //                   the counts (tiles never straddle experts, empty experts
 //                   get none) so no host synchronisation is needed.
-//   scatter_kernel  one block per chunk. Wave 0 ranks the chunk's (token,
-//                   slot) entries in order: lanes holding the same expert are
-//                   found with one ballot per expert-id bit, the rank is the
-//                   popcount of lower peer lanes, and an LDS counter per
-//                   expert carries the running position. Then all waves copy
-//                   each token row once from x and write it to its top_k
-//                   destinations with 16-byte vector accesses.
+//   scatter_kernel  grid (chunk, column split). Wave 0 ranks the chunk's
+//                   (token, slot) entries in order: lanes holding the same
+//                   expert are found with one ballot per expert-id bit, the
+//                   rank is the popcount of lower peer lanes, and an LDS
+//                   counter per expert carries the running position (split 0
+//                   writes the index outputs). Then all waves copy this
+//                   split's columns of each token row once from x to its
+//                   top_k destinations with 16-byte vector accesses. Column
+//                   splits keep enough workgroups in flight when there are
+//                   few tokens (decode).
 #include "moe_common.h"
 
 namespace astrai_moe {
@@ -138,6 +141,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     int32_t* __restrict__ sorted_token, T* __restrict__ sorted_w,
     int32_t* __restrict__ token_pos, T* __restrict__ x_perm) {
   __shared__ int cnt[ASTRAI_MOE_MAX_EXPERTS];
+  const bool write_index = blockIdx.y == 0;
   __shared__ int pos_l[ASTRAI_MOE_CHUNK_TOKENS * ASTRAI_MOE_MAX_TOPK];
   const int64_t chunk = blockIdx.x;
   const int64_t t0 = chunk * ASTRAI_MOE_CHUNK_TOKENS;
@@ -172,10 +176,12 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
       if (i < n_ent) {
         const bool ok = valid && p >= 0 && p < n_rows;
         pos_l[i] = ok ? p : -1;
-        token_pos[t0 * top_k + i] = ok ? p : -1;
-        if (ok) {
-          sorted_token[p] = (int32_t)(t0 + i / top_k);
-          sorted_w[p] = topk_w[t0 * top_k + i];
+        if (write_index) {
+          token_pos[t0 * top_k + i] = ok ? p : -1;
+          if (ok) {
+            sorted_token[p] = (int32_t)(t0 + i / top_k);
+            sorted_w[p] = topk_w[t0 * top_k + i];
+          }
         }
       }
     }
@@ -185,12 +191,14 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   // Row copy: each token row is read once and written top_k times.
   const int wave = threadIdx.x >> 6;
   constexpr int kWaves = kScatterThreads / 64;
+  const int64_t nunits = kVec ? dim * (int64_t)sizeof(T) / 16 : dim;  // 16-byte vectors or elements
+  const int64_t u0 = nunits * blockIdx.y / gridDim.y;
+  const int64_t u1 = nunits * (blockIdx.y + 1) / gridDim.y;
   if (kVec) {
     // 16-byte vectors; dim * sizeof(T) is a multiple of 16.
-    const int64_t nvec = dim * (int64_t)sizeof(T) / 16;
     for (int lt = wave; lt < nt; lt += kWaves) {
       const uint4* src = reinterpret_cast<const uint4*>(x + (t0 + lt) * dim);
-      for (int64_t v = lane; v < nvec; v += 64) {
+      for (int64_t v = u0 + lane; v < u1; v += 64) {
         const uint4 val = src[v];
         for (int k = 0; k < top_k; ++k) {
           const int p = pos_l[lt * top_k + k];
@@ -201,7 +209,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   } else {
     for (int lt = wave; lt < nt; lt += kWaves) {
       const T* src = x + (t0 + lt) * dim;
-      for (int64_t c = lane; c < dim; c += 64) {
+      for (int64_t c = u0 + lane; c < u1; c += 64) {
         const T val = src[c];
         for (int k = 0; k < top_k; ++k) {
           const int p = pos_l[lt * top_k + k];
@@ -229,15 +237,22 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
   const bool vec = (dim * (int64_t)sizeof(T)) % 16 == 0 &&
                    (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(x_perm) % 16) == 0;
+  // Column splits: aim for >= 512 workgroups, each split >= 64 units wide.
+  const int64_t nunits = vec ? dim * (int64_t)sizeof(T) / 16 : dim;
+  int64_t splits = ceil_div(512, nc);
+  if (splits > nunits / 64) splits = nunits / 64;
+  if (splits < 1) splits = 1;
+  if (splits > 65535) splits = 65535;
+  const dim3 grid((unsigned)nc, (unsigned)splits);
   if (vec)
-    hipLaunchKernelGGL((scatter_kernel<T, true>), dim3((unsigned)nc),
+    hipLaunchKernelGGL((scatter_kernel<T, true>), grid,
                        dim3(kScatterThreads), 0, s, topk_idx,
                        static_cast<const T*>(topk_w), chunk_base,
                        static_cast<const T*>(x), n_tokens, n_experts, top_k,
                        dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
                        static_cast<T*>(x_perm));
   else
-    hipLaunchKernelGGL((scatter_kernel<T, false>), dim3((unsigned)nc),
+    hipLaunchKernelGGL((scatter_kernel<T, false>), grid,
                        dim3(kScatterThreads), 0, s, topk_idx,
                        static_cast<const T*>(topk_w), chunk_base,
                        static_cast<const T*>(x), n_tokens, n_experts, top_k,

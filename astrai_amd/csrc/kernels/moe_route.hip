@@ -14,7 +14,8 @@
 //     persistent warp softmax (ATen/native/cuda/PersistentSoftmax.cuh:72-206).
 //   * top-k: the selected set is every value above the k-th largest plus the
 //     lowest-index entries equal to it; the kernel emits values in descending
-//     order (ties: lower expert first).
+//     order (ties: lower expert first), by repeated arg-max over keys that
+//     pack the probability's bits above the inverted expert id.
 //   * renorm sum: torch reduces a row of K contiguous values with
 //     bw = last_pow2(K) lanes, lane j adding elements j and j+bw, then a
 //     shfl_down tree with offsets 1, 2, 4, ... (ATen/native/cuda/Reduce.cuh:
@@ -29,7 +30,30 @@
 namespace astrai_moe {
 namespace {
 
-constexpr int kRouteThreads = 256;
+constexpr int kRouteThreads = 1024;  // 16 waves: a 32-token chunk is 2 rounds of 16 tokens at E >= 64
+
+// Packed (probability, column) keys for the top-k arg-max.
+template <typename T>
+struct KeyOf;
+template <>
+struct KeyOf<bf16_t> {  // bf16 bits above a 16-bit inverted column
+  typedef uint32_t type;
+  static constexpr int kIdxBits = 16;
+  __device__ static inline uint32_t bits(float v) { return (uint32_t)(__float_as_uint(v) >> 16); }
+  __device__ static inline float value(uint32_t b) { return __uint_as_float(b << 16); }
+  __device__ static inline uint32_t shfl_xor(uint32_t v, int off, int w) { return __shfl_xor(v, off, w); }
+};
+template <>
+struct KeyOf<float> {  // fp32 bits above a 32-bit inverted column
+  typedef uint64_t type;
+  static constexpr int kIdxBits = 32;
+  __device__ static inline uint64_t bits(float v) { return (uint64_t)__float_as_uint(v); }
+  __device__ static inline float value(uint64_t b) { return __uint_as_float((uint32_t)b); }
+  __device__ static inline uint64_t shfl_xor(uint64_t v, int off, int w) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, off, w), hi = __shfl_xor((uint32_t)(v >> 32), off, w);
+    return ((uint64_t)hi << 32) | lo;
+  }
+};
 
 template <typename T, int WS, int ITER>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
@@ -77,48 +101,43 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
 #pragma unroll
     for (int off = WS / 2; off > 0; off /= 2) sum += __shfl_xor(sum, off, WS);
     // probabilities, rounded to the activation dtype (mlp.py:84 .to(dtype)).
-    bool taken[ITER];
 #pragma unroll
     for (int it = 0; it < ITER; ++it) {
       const float p = sum == 0.0f ? NAN : el[it] / sum;
       el[it] = Elem<T>::round(p);
-      taken[it] = (lane + it * WS) >= n_experts;
     }
 
-    // top-k by repeated arg-max; lane k keeps the k-th selection.
+    // top-k by repeated arg-max over packed keys: the probability's bit
+    // pattern (non-negative floats order like their bits) above the inverted
+    // column index, so one max picks the largest value and, among equal
+    // values, the lowest column. Taken or padded columns hold key 0, below
+    // every live key, so each round picks a distinct valid column.
+    using Key = typename KeyOf<T>::type;
+    constexpr int kIdxBits = KeyOf<T>::kIdxBits;
+    constexpr Key kIdxMask = (Key(1) << kIdxBits) - 1;
+    Key key[ITER];
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int c = lane + it * WS;
+      key[it] = c < n_experts ? ((KeyOf<T>::bits(el[it]) << kIdxBits) | (kIdxMask - (Key)c)) : Key(0);
+    }
     float my_v = 0.0f;
     int my_i = 0;
     for (int k = 0; k < top_k; ++k) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
+      Key best = 0;
 #pragma unroll
-      for (int it = 0; it < ITER; ++it) {
-        const int c = lane + it * WS;
-        // The first free column is always taken as a candidate so that a row
-        // of NaNs still yields distinct, valid expert ids.
-        if (!taken[it] && (bi == 0x7fffffff || el[it] > bv)) {
-          bv = el[it];
-          bi = c;
-        }
-      }
+      for (int it = 0; it < ITER; ++it) best = key[it] > best ? key[it] : best;
 #pragma unroll
       for (int off = WS / 2; off > 0; off /= 2) {
-        const float ov = __shfl_xor(bv, off, WS);
-        const int oi = __shfl_xor(bi, off, WS);
-        const bool better =
-            (oi != 0x7fffffff) &&
-            (bi == 0x7fffffff || ov > bv || (ov == bv && oi < bi));
-        if (better) {
-          bv = ov;
-          bi = oi;
-        }
+        const Key o = KeyOf<T>::shfl_xor(best, off, WS);
+        best = o > best ? o : best;
       }
 #pragma unroll
       for (int it = 0; it < ITER; ++it)
-        if (bi == lane + it * WS) taken[it] = true;
+        if (key[it] == best) key[it] = 0;
       if (lane == k) {
-        my_v = bv;
-        my_i = bi;
+        my_i = (int)(kIdxMask - (best & kIdxMask));
+        my_v = KeyOf<T>::value(best >> kIdxBits);
       }
     }
 
