@@ -43,6 +43,9 @@
 // activation rows and expert-weight rows in that XCD's L2.
 #include "moe_gemm.h"
 
+#include <algorithm>
+#include <atomic>
+
 namespace astrai_moe {
 namespace {
 
@@ -75,7 +78,6 @@ struct TileCfg {
   static_assert(WM % 32 == 0 && WN % 64 == 0, "32x32 MFMA tiles; gate/up halves");
   static_assert(STAGES >= 2 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS");
   static_assert(DMA_PER_WAVE * (STAGES - 1) <= 63, "vmcnt range");
-  static_assert(WAVES * 32 * WN * 2 <= STAGES * STAGE_BYTES, "epilogue staging");
   // physical 16-byte chunk of logical chunk c in row r
   __device__ static inline int swz(int r) { return (r >> 1) & 7; }
 };
@@ -111,27 +113,36 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
     int capacity, bf16_t* __restrict__ C) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, MT = Cfg::MT, NT = Cfg::NT, S = Cfg::STAGES;
-  __shared__ __attribute__((aligned(1024))) char smem[S * Cfg::STAGE_BYTES];
+  constexpr int DPW = Cfg::DMA_PER_WAVE;
+  // epilogue staging: each wave stages 32-row pieces of its output tile
+  constexpr int OUTC = kGateUp ? Cfg::WN / 2 : Cfg::WN;  // output columns per wave
+  constexpr int OROW = OUTC * 2;                          // staged row bytes
+  constexpr int STAGE_AREA = S * Cfg::STAGE_BYTES;
+  static_assert(STAGE_AREA + Cfg::WAVES * 32 * OROW <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGE_AREA + Cfg::WAVES * 32 * OROW];
 
-  // ---- workgroup -> (row tile, column tile) ----
-  const int bid = blockIdx.x;
+  // ---- this workgroup's tiles ----
+  // Round r takes logical tile r * G + slot. Workgroup ids are dealt to the 8
+  // XCDs round-robin, so slot gives the workgroups of one XCD a contiguous
+  // range of logical tiles in every round; the logical order walks GM row
+  // tiles for every column tile before moving on.
   const int G = gridDim.x;
-  const int per_xcd = G / kXcds, rem = G % kXcds;
-  const int xcd = bid % kXcds;
-  const int logical = xcd * per_xcd + min(xcd, rem) + bid / kXcds;
-  const int group_size = Cfg::GM * n_tiles_n;
-  const int first_m = (logical / group_size) * Cfg::GM;
-  const int gm = min(Cfg::GM, capacity - first_m);
-  const int in_group = logical % group_size;
-  const int mt = first_m + in_group % gm;
-  const int nt = in_group / gm;
-
+  const int bid = blockIdx.x;
+  const int slot = (G % kXcds == 0) ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
+  const int total = capacity * n_tiles_n;
   const int n_live = min(tiles[0], tiles[2]);
-  if (mt >= n_live) return;
-  const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
-  const int e = ti[0];
-  const int row0 = ti[1];
-  const int rows = min(BM, ti[2] - row0);
+  const int group_size = Cfg::GM * n_tiles_n;
+  auto decode = [&](int logical, int& mt_o, int& nt_o) -> bool {
+    const int first_m = (logical / group_size) * Cfg::GM;
+    const int gm = min(Cfg::GM, capacity - first_m);
+    const int in_group = logical - (first_m / Cfg::GM) * group_size;
+    mt_o = first_m + in_group % gm;
+    nt_o = in_group / gm;
+    return mt_o < n_live;
+  };
+  int logical = slot, mt = 0, nt = 0;
+  while (logical < total && !decode(logical, mt, nt)) logical += G;
+  if (logical >= total) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -147,25 +158,33 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   // 32-bit byte offsets from uniform tile bases.
   const int dma_row = lane >> 3;
   const int dw = wave < Cfg::DMAW ? wave : 0;
-  const char* a_base = reinterpret_cast<const char*>(A + (int64_t)row0 * K);
-  const char* b_base0 = reinterpret_cast<const char*>(
-      static_cast<const bf16_t*>(W0[e]) + (int64_t)nt * (kGateUp ? BN / 2 : BN) * K);
-  const char* b_base1 =
-      kGateUp ? reinterpret_cast<const char*>(static_cast<const bf16_t*>(W1[e]) + (int64_t)nt * (BN / 2) * K)
-              : b_base0;
+  // B rows need no clamping, so their offsets are formed per op from two lane
+  // constants: row 8q + dma_row has swizzle ((q & 1) * 4 + dma_row / 2) & 7.
+  const uint32_t b_lane = (uint32_t)dma_row * (uint32_t)K * 2u;
+  const uint32_t b_chk0 = (uint32_t)(((lane & 7) ^ ((dma_row >> 1) & 7)) << 4);
+  const uint32_t b_chk1 = (uint32_t)(((lane & 7) ^ (((dma_row >> 1) + 4) & 7)) << 4);
+  // per-tile state
+  int row0 = 0, rows = 0;
+  const char* a_base = nullptr;
+  const char* b_base0 = nullptr;
+  const char* b_base1 = nullptr;
   uint32_t a_src[Cfg::A_PER_WAVE];
+  auto setup = [&](int mt_, int nt_) {
+    const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt_ * ASTRAI_MOE_TILE_STRIDE;
+    const int e = ti[0];
+    row0 = ti[1];
+    rows = min(BM, ti[2] - row0);
+    a_base = reinterpret_cast<const char*>(A + (int64_t)row0 * K);
+    b_base0 = reinterpret_cast<const char*>(static_cast<const bf16_t*>(W0[e]) +
+                                            (int64_t)nt_ * (kGateUp ? BN / 2 : BN) * K);
+    b_base1 = kGateUp ? reinterpret_cast<const char*>(static_cast<const bf16_t*>(W1[e]) + (int64_t)nt_ * (BN / 2) * K)
+                      : b_base0;
 #pragma unroll
-  for (int i = 0; i < Cfg::A_PER_WAVE; ++i) {
-    const int r = (dw * Cfg::A_PER_WAVE + i) * 8 + dma_row;
-    a_src[i] = (uint32_t)min(r, rows - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ Cfg::swz(r)) << 4);
-  }  // pad rows re-read a valid row
-  uint32_t b_src[Cfg::B_PER_WAVE];
-#pragma unroll
-  for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
-    const int r = (dw * Cfg::B_PER_WAVE + i) * 8 + dma_row;
-    const int rr = (kGateUp && r >= BN / 2) ? r - BN / 2 : r;  // up rows follow the gate rows
-    b_src[i] = (uint32_t)rr * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ Cfg::swz(r)) << 4);
-  }
+    for (int i = 0; i < Cfg::A_PER_WAVE; ++i) {
+      const int r = (dw * Cfg::A_PER_WAVE + i) * 8 + dma_row;
+      a_src[i] = (uint32_t)min(r, rows - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ Cfg::swz(r)) << 4);
+    }  // pad rows re-read a valid row
+  };
   auto issue_stage = [&](int kstep, int buf) {
     if (wave >= Cfg::DMAW) return;
     char* sa = smem + buf * Cfg::STAGE_BYTES;
@@ -176,9 +195,12 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
       lds_dma_16(a_base + (a_src[i] + koff), sa + (wave * Cfg::A_PER_WAVE + i) * 1024);
 #pragma unroll
     for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
-      const int r0 = (wave * Cfg::B_PER_WAVE + i) * 8;  // uniform
+      const int q = wave * Cfg::B_PER_WAVE + i;  // uniform 8-row group
+      const int r0 = q * 8;
       const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
-      lds_dma_16(bb + (b_src[i] + koff), sb + (wave * Cfg::B_PER_WAVE + i) * 1024);
+      const int rq = (kGateUp && r0 >= BN / 2) ? r0 - BN / 2 : r0;  // up rows follow the gate rows
+      const uint32_t off = (uint32_t)rq * (uint32_t)K * 2u + b_lane + ((q & 1) ? b_chk1 : b_chk0);
+      lds_dma_16(bb + (off + koff), sb + (wave * Cfg::B_PER_WAVE + i) * 1024);
     }
   };
 
@@ -201,28 +223,22 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     b_off[j] = (r + frag_row) * kRowBytes;
   }
   bf16x8_t fa[2][MT], fb[2][NT];
-  auto read_frags = [&](int buf, int ks, int slot) {
+  auto read_frags = [&](int buf, int ks, int slot_) {
     const char* sa = smem + buf * Cfg::STAGE_BYTES;
     const char* sb = sa + Cfg::A_BYTES;
     const int sw = ((ks * 2 + (lane >> 5)) ^ fsw) << 4;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) fa[slot][i] = *reinterpret_cast<const bf16x8_t*>(sa + a_off[i] + sw);
+    for (int i = 0; i < MT; ++i) fa[slot_][i] = *reinterpret_cast<const bf16x8_t*>(sa + a_off[i] + sw);
 #pragma unroll
-    for (int j = 0; j < NT; ++j) fb[slot][j] = *reinterpret_cast<const bf16x8_t*>(sb + b_off[j] + sw);
+    for (int j = 0; j < NT; ++j) fb[slot_][j] = *reinterpret_cast<const bf16x8_t*>(sb + b_off[j] + sw);
   };
   f32x16_t acc[MT][NT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-  auto mfmas = [&](int slot) {
+  auto mfmas = [&](int slot_) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int j = 0; j < NT; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot][i], fb[slot][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot_][i], fb[slot_][j], acc[i][j], 0, 0, 0);
   };
   // one fragment read per MFMA issue slot, then the remaining MFMAs
   auto interleave = [&]() {
@@ -234,91 +250,136 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     if constexpr (MT * NT > MT + NT) __builtin_amdgcn_sched_group_barrier(0x008, MT * NT - (MT + NT), 0);
   };
 
-  // ---- main loop ----
+  // ---- epilogue of one tile ----
+  // Accumulator element r of lane l sits at row 8*(r/4) + 4*(l/32) + r%4,
+  // column l%32 of its 32x32 tile. Each wave stages 32-row pieces of its
+  // output in its own slice of the staging area (disjoint from the stage
+  // buffers, which by then hold the next tile's first K steps) so the global
+  // stores are 16-byte row segments.
+  auto epilogue = [&](int t_row0, int t_rows, int t_nt) {
+    constexpr int SEGS = OROW / 16;  // 16-byte segments per row
+    constexpr int ROWS_PER_PASS = 64 / SEGS;
+    // Lane-derived addresses are recomputed per tile: an opaque copy of the
+    // lane id keeps the compiler from hoisting them out of the tile loop,
+    // where they would stay live (and spill) across the whole main loop.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int col_lane = el & 31;
+    const int row_lane = 4 * (el >> 5);
+    const int n_base = kGateUp ? t_nt * (BN / 2) + wn * (Cfg::WN / 2) : t_nt * BN + wn * Cfg::WN;
+    char* stage = smem + STAGE_AREA + wave * (32 * OROW);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = 8 * (r / 4) + row_lane + (r % 4);
+        if (kGateUp) {
+          constexpr int half = NT / 2;
+#pragma unroll
+          for (int j = 0; j < half; ++j) {
+            const float g = (float)(__bf16)acc[i][j][r];
+            const float u = (float)(__bf16)acc[i][j + half][r];
+            const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+            const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
+            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 32 + col_lane) * 2) = (__bf16)(u * sv);
+          }
+        } else {
+          const int gmr = wm * Cfg::WM + i * 32 + m;
+          const float w = bf16_bits_to_f32(row_w[t_row0 + min(gmr, t_rows - 1)]);
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 32 + col_lane) * 2) =
+                (__bf16)((float)(__bf16)acc[i][j][r] * w);
+        }
+      }
+      // the staging slice is private to this wave
+      wait_lds();
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
+        const int m = p * ROWS_PER_PASS + el / SEGS;
+        const int seg = el % SEGS;
+        const int gmr = wm * Cfg::WM + i * 32 + m;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
+        if (gmr < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gmr) * N + n_base + seg * 8) = v;
+      }
+      wait_lds();
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+
+  // Barriers are s_barrier after explicit waits: LDS-DMA completion is tracked
+  // by vmcnt, so the waits are placed by hand rather than by a fence.
+  auto barrier = [&]() {
+    wait_lds();
+    __builtin_amdgcn_s_barrier();
+  };
+
   const int KT = K / kBK;
+  setup(mt, nt);
 #pragma unroll
   for (int s = 0; s < S; ++s)
     if (s < KT) issue_stage(s, s);
-  wait_groups<Cfg::DMA_PER_WAVE, S - 1>(min(S - 1, KT - 1));  // step 0 landed
-  __syncthreads();
-  read_frags(0, 0, 0);
-  int buf = 0;
-  for (int kt = 0; kt < KT; ++kt) {
+  wait_groups<DPW, S - 1>(min(S - 1, KT - 1));  // step 0 landed
+  barrier();
+  while (true) {
+    // ---- main loop over K ----
 #pragma unroll
-    for (int ks = 0; ks < Cfg::KSUB; ++ks) {
-      const int slot = ks & 1;
-      if (ks < Cfg::KSUB - 1) {
-        read_frags(buf, ks + 1, slot ^ 1);
-        interleave();
-        mfmas(slot);
-      } else {
-        const int nbuf = (buf + 1 == S) ? 0 : buf + 1;
-        if (kt + 1 < KT) {
-          // step kt+1 landed (later stages may still be in flight); after the
-          // barrier every wave is done reading step kt's buffer
-          wait_groups<Cfg::DMA_PER_WAVE, S - 2>(min(S - 2, KT - 2 - kt));
-          __builtin_amdgcn_sched_barrier(0);
-          __syncthreads();
-          __builtin_amdgcn_sched_barrier(0);
-          if (kt + S < KT) issue_stage(kt + S, buf);
-          read_frags(nbuf, 0, slot ^ 1);
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    read_frags(0, 0, 0);
+    int buf = 0;
+    for (int kt = 0; kt < KT; ++kt) {
+#pragma unroll
+      for (int ks = 0; ks < Cfg::KSUB; ++ks) {
+        const int slot_ = ks & 1;
+        if (ks < Cfg::KSUB - 1) {
+          read_frags(buf, ks + 1, slot_ ^ 1);
           interleave();
+          mfmas(slot_);
+        } else {
+          const int nbuf = (buf + 1 == S) ? 0 : buf + 1;
+          if (kt + 1 < KT) {
+            // step kt+1 landed (later stages may still be in flight); after the
+            // barrier every wave is done reading step kt's buffer
+            wait_groups<DPW, S - 2>(min(S - 2, KT - 2 - kt));
+            __builtin_amdgcn_sched_barrier(0);
+            barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + S < KT) issue_stage(kt + S, buf);
+            read_frags(nbuf, 0, slot_ ^ 1);
+            interleave();
+          }
+          mfmas(slot_);
+          buf = nbuf;
         }
-        mfmas(slot);
-        buf = nbuf;
       }
     }
-  }
 
-  // ---- epilogue ----
-  // Accumulator element r of lane l sits at row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32 of its 32x32 tile.
-  constexpr int OUTC = kGateUp ? Cfg::WN / 2 : Cfg::WN;  // output columns per wave
-  constexpr int OROW = OUTC * 2;                          // staged row bytes
-  constexpr int SEGS = OROW / 16;                         // 16-byte segments per row
-  constexpr int ROWS_PER_PASS = 64 / SEGS;
-  const int col_lane = lane & 31;
-  const int row_lane = 4 * (lane >> 5);
-  const int n_base = kGateUp ? nt * (BN / 2) + wn * (Cfg::WN / 2) : nt * BN + wn * Cfg::WN;
-  __syncthreads();  // all waves are done with the stage buffers
-  char* stage = smem + wave * (32 * OROW);
+    // ---- next tile's first stages, then this tile's epilogue ----
+    int nlogical = logical + G, nmt = 0, nnt = 0;
+    while (nlogical < total && !decode(nlogical, nmt, nnt)) nlogical += G;
+    const bool has_next = nlogical < total;
+    const int t_row0 = row0, t_rows = rows, t_nt = nt;
+    __builtin_amdgcn_sched_barrier(0);
+    barrier();  // every wave is done reading the stage buffers
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_next) {
+      setup(nmt, nnt);
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int m = 8 * (r / 4) + row_lane + (r % 4);
-      if (kGateUp) {
-        constexpr int half = NT / 2;
-#pragma unroll
-        for (int j = 0; j < half; ++j) {
-          const float g = (float)(__bf16)acc[i][j][r];
-          const float u = (float)(__bf16)acc[i][j + half][r];
-          const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-          const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
-          *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 32 + col_lane) * 2) = (__bf16)(u * sv);
-        }
-      } else {
-        const int gmr = wm * Cfg::WM + i * 32 + m;
-        const float w = bf16_bits_to_f32(row_w[row0 + min(gmr, rows - 1)]);
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-          *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 32 + col_lane) * 2) =
-              (__bf16)((float)(__bf16)acc[i][j][r] * w);
-      }
+      for (int s = 0; s < S; ++s)
+        if (s < KT) issue_stage(s, s);
     }
-    // the staging area is private to this wave
-    wait_lds();
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
-      const int m = p * ROWS_PER_PASS + lane / SEGS;
-      const int seg = lane % SEGS;
-      const int gmr = wm * Cfg::WM + i * 32 + m;
-      const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
-      if (gmr < rows) *reinterpret_cast<uint4*>(C + (int64_t)(row0 + gmr) * N + n_base + seg * 8) = v;
-    }
-    wait_lds();
-    __builtin_amdgcn_wave_barrier();
+    epilogue(t_row0, t_rows, t_nt);
+    if (!has_next) break;
+    logical = nlogical;
+    mt = nmt;
+    nt = nnt;
+    wait_vmcnt<0>();  // the next tile's stages (and this wave's stores) are done
+    barrier();
   }
 }
 
@@ -331,14 +392,30 @@ using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8, 4>;
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Compute units of the current device (one persistent workgroup each).
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 template <typename Cfg, bool kGateUp>
 int launch(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
            const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
-  const int64_t grid = capacity * n_tiles_n;
-  if (grid >= (1ll << 31))
-    return fail(ASTRAI_MOE_EINVAL, "gemm: %lld workgroups exceed the grid limit", (long long)grid);
+  const int64_t total = capacity * n_tiles_n;
+  if (total >= (1ll << 31))
+    return fail(ASTRAI_MOE_EINVAL, "gemm: %lld tiles exceed the tile-index range", (long long)total);
+  // one workgroup per compute unit (the LDS footprint allows no more), each
+  // walking its share of the tile list
+  const int64_t grid = std::min<int64_t>(total, cu_count());
   hipLaunchKernelGGL((gemm_mfma_kernel<Cfg, kGateUp>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
                      static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
                      (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C));
