@@ -3,9 +3,11 @@
 // C[rows, N] = A[rows, K] . W_e[N, K]^T for every row tile of the device-built
 // tile list, e = the tile's expert. Both operands are K-contiguous (row-major
 // activations, nn.Linear [out, in] weights), which is exactly the operand
-// layout of v_mfma_f32_32x32x16_bf16: lane l supplies row (l % 32) and the
-// eight consecutive K values starting at 8 * (l / 32) of both A and B, so no
-// transposes are needed anywhere.
+// layout of v_mfma_f32_16x16x32_bf16: lane l supplies row (l % 16) and the
+// eight consecutive K values starting at 8 * (l / 16) of both A and B, so no
+// transposes are needed anywhere. (The 16x16x32 shape sustains more than the
+// 32x32x16 one on gfx950: measured 2.0-2.1 vs 1.6-1.9 PFLOP/s in a
+// register-only loop, and its results here are bit-identical.)
 //
 // Workgroup: WGM x WGN waves over a BM x BN output tile, K staged BK = 64 at a
 // time through STAGES LDS buffers. The gate/up kernel's BN columns are BN/2
@@ -25,22 +27,26 @@
 // choice of source chunk for each lane.
 //
 // Pipeline: the DMA of step k+STAGES-1 is in flight while step k computes.
-// MFMA fragments are double-buffered in registers (fragments of substep s+1
-// are read while substep s's MFMAs run, one ds_read per MFMA slot), and the
-// barrier that publishes step k+1 sits before step k's last MFMA substep so
-// its latency hides behind those MFMAs.
+// MFMA fragments are double-buffered in registers (fragments of the second
+// 32-K half of a step are read while the first half's MFMAs run), and the
+// barrier that publishes step k+1 sits before step k's second half so its
+// latency hides behind those MFMAs; after it a DMA wave reads its fragments
+// before issuing its burst of DMA ops, which hold it until the CU's vector
+// memory path accepts them.
 //
 // Epilogue: accumulators are rounded to bf16 with the hardware converter
 // (v_cvt_pk_bf16_f32, round-to-nearest-even), SiLU is g * rcp(1 + 2^(-g*log2e))
 // on v_exp_f32 / v_rcp_f32 (within 2 ulp of the libm form before its bf16
-// rounding), and each wave stages 32-row pieces of its output in LDS so the
+// rounding), and each wave stages 16-row pieces of its output in LDS so the
 // global stores are 16-byte row segments.
 //
-// Block scheduling: workgroup ids are remapped so each of the 8 XCDs (ids are
-// dealt round-robin to XCDs) gets a contiguous range of the logical tile
-// order, and the logical order walks GM row tiles for every column tile before
-// moving on, so concurrently resident workgroups on one XCD share both
-// activation rows and expert-weight rows in that XCD's L2.
+// Scheduling: one persistent workgroup per CU walks the tile list. Workgroup
+// ids are dealt round-robin to the 8 XCDs, so each XCD's workgroups take a
+// contiguous range of the logical tile order in every round, and the logical
+// order walks GM row tiles for every column tile before moving on: the
+// workgroups resident on one XCD share activation rows and expert-weight rows
+// in that XCD's L2. The first stages of a workgroup's next tile are issued
+// before the epilogue of the current one.
 #include "moe_gemm.h"
 
 #include <algorithm>
@@ -50,7 +56,6 @@ namespace astrai_moe {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 64;             // K elements per stage
 constexpr int kRowBytes = kBK * 2;  // 128 bytes per staged row
@@ -64,9 +69,6 @@ struct TileCfg {
   static constexpr int THREADS = WAVES * 64;
   static constexpr int WM = BM / WGM;  // rows per wave
   static constexpr int WN = BN / WGN;  // columns per wave
-  static constexpr int MT = WM / 32;   // 32x32 MFMA tiles per wave along M
-  static constexpr int NT = WN / 32;   // ... along N
-  static constexpr int KSUB = kBK / 16;
   static constexpr int A_BYTES = BM * kRowBytes;
   static constexpr int B_BYTES = BN * kRowBytes;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
@@ -75,7 +77,7 @@ struct TileCfg {
   static constexpr int DMA_PER_WAVE = A_PER_WAVE + B_PER_WAVE;
   static_assert(DMAW >= 1 && DMAW <= WAVES, "DMA waves");
   static_assert(A_BYTES % (1024 * DMAW) == 0 && B_BYTES % (1024 * DMAW) == 0, "DMA ops split over waves");
-  static_assert(WM % 32 == 0 && WN % 64 == 0, "32x32 MFMA tiles; gate/up halves");
+  static_assert(WM % 16 == 0 && WN % 32 == 0, "16x16 MFMA tiles; gate/up halves");
   static_assert(STAGES >= 2 && STAGES * STAGE_BYTES <= 160 * 1024, "LDS");
   static_assert(DMA_PER_WAVE * (STAGES - 1) <= 63, "vmcnt range");
   // physical 16-byte chunk of logical chunk c in row r
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
     int capacity, bf16_t* __restrict__ C) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, MT = Cfg::MT, NT = Cfg::NT, S = Cfg::STAGES;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, S = Cfg::STAGES;
   constexpr int DPW = Cfg::DMA_PER_WAVE;
   // epilogue staging: each wave stages 32-row pieces of its output tile
   constexpr int OUTC = kGateUp ? Cfg::WN / 2 : Cfg::WN;  // output columns per wave
@@ -157,18 +159,11 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   // fetches the logical chunk stored at that physical chunk. Sources are
   // 32-bit byte offsets from uniform tile bases.
   const int dma_row = lane >> 3;
-  const int dw = wave < Cfg::DMAW ? wave : 0;
-  // B rows need no clamping, so their offsets are formed per op from two lane
-  // constants: row 8q + dma_row has swizzle ((q & 1) * 4 + dma_row / 2) & 7.
-  const uint32_t b_lane = (uint32_t)dma_row * (uint32_t)K * 2u;
-  const uint32_t b_chk0 = (uint32_t)(((lane & 7) ^ ((dma_row >> 1) & 7)) << 4);
-  const uint32_t b_chk1 = (uint32_t)(((lane & 7) ^ (((dma_row >> 1) + 4) & 7)) << 4);
   // per-tile state
   int row0 = 0, rows = 0;
   const char* a_base = nullptr;
   const char* b_base0 = nullptr;
   const char* b_base1 = nullptr;
-  uint32_t a_src[Cfg::A_PER_WAVE];
   auto setup = [&](int mt_, int nt_) {
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt_ * ASTRAI_MOE_TILE_STRIDE;
     const int e = ti[0];
@@ -179,127 +174,127 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
                                             (int64_t)nt_ * (kGateUp ? BN / 2 : BN) * K);
     b_base1 = kGateUp ? reinterpret_cast<const char*>(static_cast<const bf16_t*>(W1[e]) + (int64_t)nt_ * (BN / 2) * K)
                       : b_base0;
-#pragma unroll
-    for (int i = 0; i < Cfg::A_PER_WAVE; ++i) {
-      const int r = (dw * Cfg::A_PER_WAVE + i) * 8 + dma_row;
-      a_src[i] = (uint32_t)min(r, rows - 1) * (uint32_t)K * 2u + (uint32_t)(((lane & 7) ^ Cfg::swz(r)) << 4);
-    }  // pad rows re-read a valid row
   };
+  // The source offsets are recomputed at every issue from an opaque copy of the
+  // lane's row: hoisted out of the K loop they would hold 16 VGPRs for its
+  // whole length, and the register file is full.
   auto issue_stage = [&](int kstep, int buf) {
     if (wave >= Cfg::DMAW) return;
     char* sa = smem + buf * Cfg::STAGE_BYTES;
     char* sb = sa + Cfg::A_BYTES;
     const uint32_t koff = kstep * kRowBytes;
+    int dr = dma_row;
+    asm volatile("" : "+v"(dr));
+    const uint32_t k2 = (uint32_t)K * 2u;
+    const uint32_t chk0 = (uint32_t)(((lane & 7) ^ ((dr >> 1) & 7)) << 4) + koff;
+    const uint32_t chk1 = (uint32_t)(((lane & 7) ^ (((dr >> 1) + 4) & 7)) << 4) + koff;
 #pragma unroll
-    for (int i = 0; i < Cfg::A_PER_WAVE; ++i)
-      lds_dma_16(a_base + (a_src[i] + koff), sa + (wave * Cfg::A_PER_WAVE + i) * 1024);
+    for (int i = 0; i < Cfg::A_PER_WAVE; ++i) {
+      const int q = wave * Cfg::A_PER_WAVE + i;  // uniform 8-row group
+      // pad rows past the tile's last row re-read that row
+      const uint32_t row = (uint32_t)min(q * 8 + dr, rows - 1);
+      lds_dma_16(a_base + (row * k2 + ((q & 1) ? chk1 : chk0)), sa + (wave * Cfg::A_PER_WAVE + i) * 1024);
+    }
+    const uint32_t b_row = (uint32_t)dr * k2;
 #pragma unroll
     for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
       const int q = wave * Cfg::B_PER_WAVE + i;  // uniform 8-row group
       const int r0 = q * 8;
       const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
       const int rq = (kGateUp && r0 >= BN / 2) ? r0 - BN / 2 : r0;  // up rows follow the gate rows
-      const uint32_t off = (uint32_t)rq * (uint32_t)K * 2u + b_lane + ((q & 1) ? b_chk1 : b_chk0);
-      lds_dma_16(bb + (off + koff), sb + (wave * Cfg::B_PER_WAVE + i) * 1024);
+      lds_dma_16(bb + ((uint32_t)rq * k2 + b_row + ((q & 1) ? chk1 : chk0)), sb + (wave * Cfg::B_PER_WAVE + i) * 1024);
     }
   };
 
-  // ---- MFMA fragment reads ----
-  const int frag_row = lane & 31;
-  const int fsw = Cfg::swz(frag_row);  // row bases are multiples of 32
-  int a_off[MT];
+  // ---- MFMA fragment reads (16x16x32: lane l holds row l % 16, K 8*(l/16)..+7) ----
+  constexpr int MT16 = Cfg::WM / 16, NT16 = Cfg::WN / 16;
+  const int frag_row = lane & 15;
+  const int fq = lane >> 4;
+  const int fsw = Cfg::swz(frag_row);  // row bases are multiples of 16
+  int a_off[MT16];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) a_off[i] = (wm * Cfg::WM + i * 32 + frag_row) * kRowBytes;
-  int b_off[NT];
+  for (int i = 0; i < MT16; ++i) a_off[i] = (wm * Cfg::WM + i * 16 + frag_row) * kRowBytes;
+  int b_off[NT16];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
+  for (int j = 0; j < NT16; ++j) {
     int r;
     if (kGateUp) {
-      constexpr int half = NT / 2;
-      r = (j < half) ? wn * (Cfg::WN / 2) + j * 32 : BN / 2 + wn * (Cfg::WN / 2) + (j - half) * 32;
+      constexpr int half = NT16 / 2;
+      r = (j < half) ? wn * (Cfg::WN / 2) + j * 16 : BN / 2 + wn * (Cfg::WN / 2) + (j - half) * 16;
     } else {
-      r = wn * Cfg::WN + j * 32;
+      r = wn * Cfg::WN + j * 16;
     }
     b_off[j] = (r + frag_row) * kRowBytes;
   }
-  bf16x8_t fa[2][MT], fb[2][NT];
-  auto read_frags = [&](int buf, int ks, int slot_) {
+  bf16x8_t fa[2][MT16], fb[2][NT16];
+  auto read_frags = [&](int buf, int kh, int slot_) {
     const char* sa = smem + buf * Cfg::STAGE_BYTES;
     const char* sb = sa + Cfg::A_BYTES;
-    const int sw = ((ks * 2 + (lane >> 5)) ^ fsw) << 4;
+    const int sw = ((kh * 4 + fq) ^ fsw) << 4;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) fa[slot_][i] = *reinterpret_cast<const bf16x8_t*>(sa + a_off[i] + sw);
+    for (int i = 0; i < MT16; ++i) fa[slot_][i] = *reinterpret_cast<const bf16x8_t*>(sa + a_off[i] + sw);
 #pragma unroll
-    for (int j = 0; j < NT; ++j) fb[slot_][j] = *reinterpret_cast<const bf16x8_t*>(sb + b_off[j] + sw);
+    for (int j = 0; j < NT16; ++j) fb[slot_][j] = *reinterpret_cast<const bf16x8_t*>(sb + b_off[j] + sw);
   };
-  f32x16_t acc[MT][NT];
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  f32x4_t acc[MT16][NT16];
   auto mfmas = [&](int slot_) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MT16; ++i)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[slot_][i], fb[slot_][j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < NT16; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[slot_][i], fb[slot_][j], acc[i][j], 0, 0, 0);
   };
-  // one fragment read per MFMA issue slot, then the remaining MFMAs
   auto interleave = [&]() {
 #pragma unroll
-    for (int q = 0; q < MT + NT; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    for (int q = 0; q < MT16 + NT16; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
-    if constexpr (MT * NT > MT + NT) __builtin_amdgcn_sched_group_barrier(0x008, MT * NT - (MT + NT), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, MT16 * NT16 - (MT16 + NT16), 0);
   };
 
-  // ---- epilogue of one tile ----
-  // Accumulator element r of lane l sits at row 8*(r/4) + 4*(l/32) + r%4,
-  // column l%32 of its 32x32 tile. Each wave stages 32-row pieces of its
-  // output in its own slice of the staging area (disjoint from the stage
-  // buffers, which by then hold the next tile's first K steps) so the global
-  // stores are 16-byte row segments.
+  // ---- epilogue of one tile (16-row pieces) ----
   auto epilogue = [&](int t_row0, int t_rows, int t_nt) {
-    constexpr int SEGS = OROW / 16;  // 16-byte segments per row
+    constexpr int SEGS = OROW / 16;
     constexpr int ROWS_PER_PASS = 64 / SEGS;
-    // Lane-derived addresses are recomputed per tile: an opaque copy of the
-    // lane id keeps the compiler from hoisting them out of the tile loop,
-    // where they would stay live (and spill) across the whole main loop.
     int el = lane;
     asm volatile("" : "+v"(el));
-    const int col_lane = el & 31;
-    const int row_lane = 4 * (el >> 5);
+    const int col_lane = el & 15;
+    const int row_lane = 4 * (el >> 4);
     const int n_base = kGateUp ? t_nt * (BN / 2) + wn * (Cfg::WN / 2) : t_nt * BN + wn * Cfg::WN;
     char* stage = smem + STAGE_AREA + wave * (32 * OROW);
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
+    for (int i = 0; i < MT16; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = 8 * (r / 4) + row_lane + (r % 4);
+      for (int r = 0; r < 4; ++r) {
+        const int m = row_lane + r;
         if (kGateUp) {
-          constexpr int half = NT / 2;
+          constexpr int half = NT16 / 2;
 #pragma unroll
           for (int j = 0; j < half; ++j) {
             const float g = (float)(__bf16)acc[i][j][r];
             const float u = (float)(__bf16)acc[i][j + half][r];
             const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
             const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
-            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 32 + col_lane) * 2) = (__bf16)(u * sv);
+            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 16 + col_lane) * 2) = (__bf16)(u * sv);
           }
         } else {
-          const int gmr = wm * Cfg::WM + i * 32 + m;
+          const int gmr = wm * Cfg::WM + i * 16 + m;
           const float w = bf16_bits_to_f32(row_w[t_row0 + min(gmr, t_rows - 1)]);
 #pragma unroll
-          for (int j = 0; j < NT; ++j)
-            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 32 + col_lane) * 2) =
+          for (int j = 0; j < NT16; ++j)
+            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 16 + col_lane) * 2) =
                 (__bf16)((float)(__bf16)acc[i][j][r] * w);
         }
       }
-      // the staging slice is private to this wave
       wait_lds();
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int p = 0; p < 32 / ROWS_PER_PASS; ++p) {
+      for (int p = 0; p < 16 / ROWS_PER_PASS; ++p) {
         const int m = p * ROWS_PER_PASS + el / SEGS;
         const int seg = el % SEGS;
-        const int gmr = wm * Cfg::WM + i * 32 + m;
+        const int gmr = wm * Cfg::WM + i * 16 + m;
         const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
         if (gmr < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gmr) * N + n_base + seg * 8) = v;
       }
@@ -325,38 +320,32 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   while (true) {
     // ---- main loop over K ----
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+    for (int i = 0; i < MT16; ++i)
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+      for (int j = 0; j < NT16; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
     read_frags(0, 0, 0);
     int buf = 0;
     for (int kt = 0; kt < KT; ++kt) {
-#pragma unroll
-      for (int ks = 0; ks < Cfg::KSUB; ++ks) {
-        const int slot_ = ks & 1;
-        if (ks < Cfg::KSUB - 1) {
-          read_frags(buf, ks + 1, slot_ ^ 1);
-          interleave();
-          mfmas(slot_);
-        } else {
-          const int nbuf = (buf + 1 == S) ? 0 : buf + 1;
-          if (kt + 1 < KT) {
-            // step kt+1 landed (later stages may still be in flight); after the
-            // barrier every wave is done reading step kt's buffer
-            wait_groups<DPW, S - 2>(min(S - 2, KT - 2 - kt));
-            __builtin_amdgcn_sched_barrier(0);
-            barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            if (kt + S < KT) issue_stage(kt + S, buf);
-            read_frags(nbuf, 0, slot_ ^ 1);
-            interleave();
-          }
-          mfmas(slot_);
-          buf = nbuf;
-        }
+      read_frags(buf, 1, 1);
+      interleave();
+      mfmas(0);
+      const int nbuf = (buf + 1 == S) ? 0 : buf + 1;
+      if (kt + 1 < KT) {
+        wait_groups<DPW, S - 2>(min(S - 2, KT - 2 - kt));
+        __builtin_amdgcn_sched_barrier(0);
+        barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // this wave's fragments first, so they are in flight while the DMA ops
+        // wait for the vector memory path
+        read_frags(nbuf, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + S < KT) issue_stage(kt + S, buf);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      mfmas(1);
+      buf = nbuf;
     }
 
     // ---- next tile's first stages, then this tile's epilogue ----
