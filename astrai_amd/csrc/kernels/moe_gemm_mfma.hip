@@ -179,7 +179,9 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   // lane's row: hoisted out of the K loop they would hold 16 VGPRs for its
   // whole length, and the register file is full.
   auto issue_stage = [&](int kstep, int buf) {
-    if (wave >= Cfg::DMAW) return;
+    if constexpr (Cfg::DMAW < Cfg::WAVES) {
+      if (wave >= Cfg::DMAW) return;
+    }
     char* sa = smem + buf * Cfg::STAGE_BYTES;
     char* sb = sa + Cfg::A_BYTES;
     const uint32_t koff = kstep * kRowBytes;
