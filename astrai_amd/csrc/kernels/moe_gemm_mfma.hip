@@ -37,8 +37,9 @@
 // Epilogue: accumulators are rounded to bf16 with the hardware converter
 // (v_cvt_pk_bf16_f32, round-to-nearest-even), SiLU is g * rcp(1 + 2^(-g*log2e))
 // on v_exp_f32 / v_rcp_f32 (within 2 ulp of the libm form before its bf16
-// rounding), and each wave stages 16-row pieces of its output in LDS so the
-// global stores are 16-byte row segments.
+// rounding). The weight fragment is the MFMA's first operand, which leaves
+// each lane 4 consecutive output columns of one row; each wave stages
+// 16-row pieces in LDS with 8-byte writes and stores 16-byte row segments.
 //
 // Scheduling: one persistent workgroup per CU walks the tile list. Workgroup
 // ids are dealt round-robin to the 8 XCDs, so each XCD's workgroups take a
@@ -47,6 +48,9 @@
 // workgroups resident on one XCD share activation rows and expert-weight rows
 // in that XCD's L2. The first stages of a workgroup's next tile are issued
 // before the epilogue of the current one.
+//
+// Accumulator layout (16x16x32 with operands (W, A)): lane l, element r of
+// tile (i, j) is output row 16 i + l % 16, column 16 j + 4 (l / 16) + r.
 #include "moe_gemm.h"
 
 #include <algorithm>
@@ -116,12 +120,11 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     int capacity, bf16_t* __restrict__ C) {
   constexpr int BM = Cfg::BM, BN = Cfg::BN, S = Cfg::STAGES;
   constexpr int DPW = Cfg::DMA_PER_WAVE;
-  // epilogue staging: each wave stages 32-row pieces of its output tile
-  constexpr int OUTC = kGateUp ? Cfg::WN / 2 : Cfg::WN;  // output columns per wave
-  constexpr int OROW = OUTC * 2;                          // staged row bytes
   constexpr int STAGE_AREA = S * Cfg::STAGE_BYTES;
-  static_assert(STAGE_AREA + Cfg::WAVES * 32 * OROW <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) char smem[STAGE_AREA + Cfg::WAVES * 32 * OROW];
+  constexpr int OUTC = kGateUp ? Cfg::WN / 2 : Cfg::WN;  // output columns per wave
+  constexpr int OROW = OUTC * 2 + 16;                     // staged row bytes (padded)
+  static_assert(STAGE_AREA + Cfg::WAVES * 16 * OROW <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGE_AREA + Cfg::WAVES * 16 * OROW];
 
   // ---- this workgroup's tiles ----
   // Round r takes logical tile r * G + slot. Workgroup ids are dealt to the 8
@@ -245,7 +248,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     for (int i = 0; i < MT16; ++i)
 #pragma unroll
       for (int j = 0; j < NT16; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[slot_][i], fb[slot_][j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[slot_][j], fa[slot_][i], acc[i][j], 0, 0, 0);
   };
   auto interleave = [&]() {
 #pragma unroll
@@ -256,49 +259,56 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     __builtin_amdgcn_sched_group_barrier(0x008, MT16 * NT16 - (MT16 + NT16), 0);
   };
 
-  // ---- epilogue of one tile (16-row pieces) ----
+  // ---- epilogue of one tile ----
+  // With the weight fragment as the MFMA's first operand, lane l holds output
+  // row l % 16 of its 16x16 tile and the 4 consecutive columns 4 * (l / 16)..+3.
+  // Each wave stages 16-row pieces in its own LDS slice with 8-byte writes
+  // (rows padded by 16 bytes, which spreads the 16 rows of a write over
+  // distinct banks) and stores them as 16-byte row segments.
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
   auto epilogue = [&](int t_row0, int t_rows, int t_nt) {
-    constexpr int SEGS = OROW / 16;
-    constexpr int ROWS_PER_PASS = 64 / SEGS;
     int el = lane;
     asm volatile("" : "+v"(el));
-    const int col_lane = el & 15;
-    const int row_lane = 4 * (el >> 4);
+    const int row_l = el & 15;
+    const int col_l = 4 * (el >> 4);
     const int n_base = kGateUp ? t_nt * (BN / 2) + wn * (Cfg::WN / 2) : t_nt * BN + wn * Cfg::WN;
-    char* stage = smem + STAGE_AREA + wave * (32 * OROW);
+    char* stage = smem + STAGE_AREA + wave * (16 * OROW);
 #pragma unroll
     for (int i = 0; i < MT16; ++i) {
+      const int gmr = wm * Cfg::WM + i * 16 + row_l;
+      const int srow = t_row0 + min(gmr, t_rows - 1);
+      constexpr int NJ = kGateUp ? NT16 / 2 : NT16;
+      float w = 1.0f;
+      if (!kGateUp) w = bf16_bits_to_f32(row_w[srow]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = row_lane + r;
-        if (kGateUp) {
-          constexpr int half = NT16 / 2;
+      for (int j = 0; j < NJ; ++j) {
+        bf16x4_t o;
 #pragma unroll
-          for (int j = 0; j < half; ++j) {
+        for (int r = 0; r < 4; ++r) {
+          if (kGateUp) {
             const float g = (float)(__bf16)acc[i][j][r];
-            const float u = (float)(__bf16)acc[i][j + half][r];
+            const float u = (float)(__bf16)acc[i][j + NJ][r];
             const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
             const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
-            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 16 + col_lane) * 2) = (__bf16)(u * sv);
+            o[r] = (__bf16)(u * sv);
+          } else {
+            o[r] = (__bf16)((float)(__bf16)acc[i][j][r] * w);
           }
-        } else {
-          const int gmr = wm * Cfg::WM + i * 16 + m;
-          const float w = bf16_bits_to_f32(row_w[t_row0 + min(gmr, t_rows - 1)]);
-#pragma unroll
-          for (int j = 0; j < NT16; ++j)
-            *reinterpret_cast<__bf16*>(stage + m * OROW + (j * 16 + col_lane) * 2) =
-                (__bf16)((float)(__bf16)acc[i][j][r] * w);
         }
+        *reinterpret_cast<bf16x4_t*>(stage + row_l * OROW + (j * 16 + col_l) * 2) = o;
       }
+      // the staging slice is private to this wave: 16 rows back out as 16-byte row segments
+      constexpr int SEGS = OUTC * 2 / 16;
+      constexpr int RPP = 64 / SEGS;
       wait_lds();
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int p = 0; p < 16 / ROWS_PER_PASS; ++p) {
-        const int m = p * ROWS_PER_PASS + el / SEGS;
+      for (int p = 0; p < 16 / RPP; ++p) {
+        const int m = p * RPP + el / SEGS;
         const int seg = el % SEGS;
-        const int gmr = wm * Cfg::WM + i * 16 + m;
+        const int gm = wm * Cfg::WM + i * 16 + m;
         const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
-        if (gmr < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gmr) * N + n_base + seg * 8) = v;
+        if (gm < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gm) * N + n_base + seg * 8) = v;
       }
       wait_lds();
       __builtin_amdgcn_wave_barrier();
