@@ -1,0 +1,126 @@
+"""Autograd for the MoE layer: HIP kernels forward, recompute backward.
+
+The reference layer is plain torch, so autograd differentiates it op by op
+(``astrai/model/components/mlp.py:22-25, 64-100``). Here the forward runs on
+the HIP kernels; the backward recomputes each expert's SwiGLU with the same
+torch ops as ``mlp.py:22-25`` and lets autograd differentiate them (the
+recompute that gradient checkpointing would do anyway), so the gradient
+formulas and their rounding points are the reference's:
+
+* ``out.index_add_(0, tok, y * w)`` (``mlp.py:98``): the gradient reaching
+  expert row r is ``dout[tok(r)]``; the row's output gets ``dout * w`` and its
+  routing weight gets ``sum(dout * y)`` over the model dimension;
+* ``x[tok]`` (``mlp.py:95``): the per-row input gradients are summed back into
+  their tokens in ascending expert order, rounding after every add, which is
+  the combine kernel's contract (the reference's ``index_add_`` backward);
+* experts without rows get no gradient (the reference skips them, so their
+  ``.grad`` stays ``None`` there too).
+
+The expert GEMMs of the backward are per-expert library GEMMs (torch
+``F.linear``); the row gather/scatter runs on the HIP kernels.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from astrai_amd.extension import ops
+
+
+def _expert_forward(x: Tensor, wg: Tensor, wu: Tensor, wd: Tensor) -> Tensor:
+    """``down(up(x) * silu(gate(x)))`` with mlp.py:22-25's evaluation order."""
+    return F.linear(F.linear(x, wu) * F.silu(F.linear(x, wg)), wd)
+
+
+def _expert_grads(x: Tensor, wg: Tensor, wu: Tensor, wd: Tensor, dz: Tensor | None, z_out: bool = False):
+    """Recompute one expert on detached leaves and differentiate it."""
+    with torch.enable_grad():
+        leaves = [t.detach().requires_grad_(True) for t in (x, wg, wu, wd)]
+        z = _expert_forward(*leaves)
+    if dz is None:
+        return z.detach()
+    grads = torch.autograd.grad(z, leaves, dz)
+    return (z.detach(), grads) if z_out else grads
+
+
+class RoutedExperts(torch.autograd.Function):
+    """Routed experts and their weighted combine (mlp.py:89-100).
+
+    ``forward(x [T, D], topk_w [T, K], topk_idx [T, K] int32, chunk_hist,
+    tables, dim_ffn, *weights)`` where ``weights`` are the E gate, then the E
+    up, then the E down weight tensors whose device pointers ``tables`` hold.
+    Differentiable in ``x``, ``topk_w`` and every weight.
+    """
+
+    @staticmethod
+    def forward(ctx, x, topk_w, topk_idx, chunk_hist, tables, dim_ffn, *weights):
+        n_experts = len(weights) // 3
+        n_tokens, dim = x.shape
+        top_k = topk_idx.shape[1]
+        tg, tu, td = tables
+        block_m = ops.select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
+        route = ops.RouteResult(topk_idx, topk_w.contiguous(), chunk_hist)
+        perm = ops.moe_permute(route, x, n_experts, block_m)
+        h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn, block_m)
+        y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_experts, dim, block_m)
+        out = ops.moe_combine(y, perm.token_pos)
+        ctx.n_experts = n_experts
+        ctx.save_for_backward(perm.x_perm, perm.sorted_token, perm.sorted_w, perm.token_pos, perm.expert_offsets,
+                              *weights)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x_perm, sorted_token, sorted_w, token_pos, offsets, *weights = ctx.saved_tensors
+        n_experts = ctx.n_experts
+        wg, wu, wd = weights[:n_experts], weights[n_experts:2 * n_experts], weights[2 * n_experts:]
+        dout = dout.contiguous()
+        # gradient of index_add_'s source: the token's output gradient per permuted row
+        dp = dout.index_select(0, sorted_token.long())
+        dx_perm = torch.empty_like(x_perm)
+        dw_rows = torch.empty(x_perm.shape[0], dtype=dout.dtype, device=dout.device)
+        g_gate: list[Tensor | None] = [None] * n_experts
+        g_up: list[Tensor | None] = [None] * n_experts
+        g_down: list[Tensor | None] = [None] * n_experts
+        bounds = offsets.tolist()  # one host sync per backward
+        for e in range(n_experts):
+            a, b = bounds[e], bounds[e + 1]
+            if a == b:
+                continue
+            dp_e = dp[a:b]
+            w_e = sorted_w[a:b].unsqueeze(-1)
+            z, (gx, gg, gu, gd) = _expert_grads(x_perm[a:b], wg[e], wu[e], wd[e], dp_e * w_e, z_out=True)
+            dw_rows[a:b] = (dp_e * z).sum(-1)
+            dx_perm[a:b] = gx
+            g_gate[e], g_up[e], g_down[e] = gg, gu, gd
+        dx = ops.moe_combine(dx_perm, token_pos)
+        dw = dw_rows[token_pos.long()]
+        return (dx, dw, None, None, None, None, *g_gate, *g_up, *g_down)
+
+
+class DenseExpert(torch.autograd.Function):
+    """One dense SwiGLU expert (mlp.py:22-25, the shared experts and ``MLP``):
+    ``forward(x [T, D], tables, dim_ffn, w_gate, w_up, w_down)``."""
+
+    @staticmethod
+    def forward(ctx, x, tables, dim_ffn, wg, wu, wd):
+        tg, tu, td = tables
+        ctx.save_for_backward(x, wg, wu, wd)
+        return ops.moe_dense_mlp(x, tg, tu, td, dim_ffn)
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, wg, wu, wd = ctx.saved_tensors
+        gx, gg, gu, gd = _expert_grads(x, wg, wu, wd, dout.contiguous())
+        return gx, None, None, gg, gu, gd
+
+
+def routing_weights(logits: Tensor, topk_idx: Tensor, dtype: torch.dtype) -> Tensor:
+    """The renormalised top-k weights as differentiable torch ops
+    (mlp.py:84-87), evaluated at the route kernel's indices: the same values
+    the kernel produces, with autograd's path back to the logits."""
+    probs = torch.softmax(logits.float(), dim=-1).to(dtype)
+    w = probs.gather(1, topk_idx.long())
+    return w / w.sum(dim=-1, keepdim=True)

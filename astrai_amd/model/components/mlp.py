@@ -20,9 +20,10 @@ combine and the shared-expert mean — runs in the HIP kernels of
 ``astrai_amd.extension`` with the reference's rounding points.
 
 The HIP path is the only path: inputs it cannot take (CPU tensors, dtypes
-other than float32/bfloat16, autograd through the layer, experts whose
-``up/gate/down`` are not bias-free ``Linear`` modules, e.g. after LoRA
-injection) raise instead of silently running something else.
+other than float32/bfloat16, experts whose ``up/gate/down`` are not bias-free
+``Linear`` modules, e.g. after LoRA injection) raise instead of silently
+running something else. With autograd active the forward still runs on the
+kernels and the backward recomputes the experts (``autograd.py``).
 """
 
 from __future__ import annotations
@@ -33,6 +34,7 @@ from torch import Tensor
 
 from astrai_amd.extension import ops
 from astrai_amd.factory import BaseFactory
+from astrai_amd.model.components.autograd import DenseExpert, RoutedExperts, routing_weights
 from astrai_amd.model.components.linear import Linear
 
 
@@ -48,10 +50,10 @@ def _check_gpu_input(x: Tensor, params: list[Tensor], who: str) -> None:
     for p in params:
         if p.device != x.device or p.dtype != x.dtype:
             raise RuntimeError(f"{who}: parameters must be on {x.device} in {x.dtype}, found {p.device}/{p.dtype}")
-    if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in params)):
-        raise NotImplementedError(
-            f"{who} implements the forward pass only; run it under torch.no_grad() or torch.inference_mode()"
-        )
+
+
+def _needs_grad(x: Tensor, params: list[Tensor]) -> bool:
+    return torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in params))
 
 
 def _plain_linear(m: nn.Module, who: str) -> Tensor:
@@ -82,8 +84,11 @@ class MLP(nn.Module):
         _check_gpu_input(x, [wg, wu, wd], "MLP")
         lead, dim = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, dim).contiguous()
-        tables = [ops.expert_weight_table([w], tuple(w.shape)) for w in (wg, wu, wd)]
-        out = ops.moe_dense_mlp(x2, *tables, wg.shape[0])
+        tables = tuple(ops.expert_weight_table([w], tuple(w.shape)) for w in (wg, wu, wd))
+        if _needs_grad(x2, [wg, wu, wd]):
+            out = DenseExpert.apply(x2, tables, wg.shape[0], wg, wu, wd)
+        else:
+            out = ops.moe_dense_mlp(x2, *tables, wg.shape[0])
         return out.view(*lead, dim)
 
 
@@ -154,10 +159,10 @@ class DeepSeekMoE(nn.Module):
     def forward(self, x: Tensor) -> Tensor:
         bsz, seq_len, dim = x.shape
         x_flat = x.view(-1, dim)
-        params = [self.router.weight] + [p for p in self.routed_experts.parameters()] + [
-            p for p in self.shared_experts.parameters()
-        ]
+        params = list(self.parameters())
         _check_gpu_input(x_flat, params, "DeepSeekMoE")
+        if _needs_grad(x_flat, params):
+            return self._forward_autograd(x_flat).view(bsz, seq_len, dim)
         shared_out = self._shared_forward(x_flat)
         out = self._routed_forward(x_flat, shared_out)
         return out.view(bsz, seq_len, dim)
@@ -180,3 +185,28 @@ class DeepSeekMoE(nn.Module):
         logits = self.router(x)
         dim_ffn = self.routed_experts[0].up.weight.shape[0]
         return ops.moe_routed_forward(x, logits, tg, tu, td, dim_ffn, self.n_activated_experts, shared)
+
+    def _forward_autograd(self, x: Tensor) -> Tensor:
+        """mlp.py:64-100 with autograd: kernels forward, recompute backward.
+        Routing indices come from the route kernel; the weights are rebuilt
+        from the logits with torch ops (same values) so their gradient reaches
+        the router."""
+        n_tokens = x.shape[0]
+        if n_tokens == 0:
+            return x.new_empty(0, x.shape[1])
+        t_routed, t_shared = self._weight_tables()
+        routed_w = self._expert_weights(self.routed_experts)
+        dim_ffn = routed_w[0][0].shape[0]
+        logits = self.router(x)
+        route = ops.moe_route(logits.detach(), self.n_activated_experts)
+        topk_w = routing_weights(logits, route.topk_idx, x.dtype)
+        routed = RoutedExperts.apply(x, topk_w, route.topk_idx, route.chunk_hist, t_routed, dim_ffn,
+                                     *routed_w[0], *routed_w[1], *routed_w[2])
+        if self.n_shared_experts == 0:
+            return routed
+        shared_w = self._expert_weights(self.shared_experts)
+        shared = sum(
+            DenseExpert.apply(x, t_shared[i], dim_ffn, shared_w[0][i], shared_w[1][i], shared_w[2][i])
+            for i in range(self.n_shared_experts)
+        ) / self.n_shared_experts
+        return shared + routed

@@ -1,0 +1,165 @@
+"""Backward parity: gradients of DeepSeekMoE / MLP (HIP kernels forward,
+recompute backward) vs autograd through the oracle (the reference's torch
+forward, mlp.py:14-25 and 64-100) with the same parameters, input and output
+gradient, on the same device.
+
+The expert weight gradients come from the same torch ops on the same rows as
+the oracle's; the input gradient is the reference's index_add_ order
+(ascending expert) but autograd may add the router, shared and routed
+contributions in another order, so everything is compared with the layer's
+tolerance: elementwise |g - ref| <= atol + rtol * |ref| with atol scaled to
+the tensor (1e-3 of its largest magnitude in bf16, 1e-6 in fp32), >= 99.9 %
+of the elements passing and the worst error below 5 % (bf16) / 1e-4 (fp32)
+of the largest magnitude. Experts that receive no token must get no gradient,
+as in the reference.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from astrai_amd.model.components.mlp import MLP, DeepSeekMoE
+from astrai_amd.workloads import WORKLOADS, make_layer
+from oracle import moe_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, ref, dtype, label):
+    assert got is not None and ref is not None, f"{label}: missing gradient"
+    got, ref = got.float(), ref.float()
+    scale = ref.abs().max().item() or 1.0
+    if dtype == torch.bfloat16:
+        rtol, atol, worst_frac = 2e-2, 1e-3 * scale, 5e-2
+    else:
+        rtol, atol, worst_frac = 1e-4, 1e-6 * scale, 1e-4
+    err = (got - ref).abs()
+    frac = (err <= atol + rtol * ref.abs()).float().mean().item()
+    worst = err.max().item()
+    assert frac >= 0.999, f"{label}: {frac:.5f} of elements within tolerance (max err {worst:.3e}, scale {scale:.3e})"
+    assert worst <= worst_frac * scale, f"{label}: max err {worst:.3e} vs scale {scale:.3e}"
+
+
+def _leaf(t):
+    return t.detach().clone().requires_grad_(True)
+
+
+def _oracle(layer, x, dout):
+    rw = _leaf(layer.router.weight)
+    rb = _leaf(layer.router.bias) if getattr(layer.router, "bias", None) is not None else None
+
+    def ew(m):
+        return R.ExpertWeights(_leaf(m.gate.weight), _leaf(m.up.weight), _leaf(m.down.weight))
+
+    experts = [ew(m) for m in layer.routed_experts]
+    shared = [ew(m) for m in layer.shared_experts]
+    xl = _leaf(x)
+    out = R.moe_forward(xl, rw, rb, experts, shared, layer.n_activated_experts)
+    out.backward(dout)
+    return out.detach(), xl.grad, rw.grad, (rb.grad if rb is not None else None), experts, shared
+
+
+def _check_moe(layer, x, label, seed=0):
+    g = torch.Generator(device=x.device).manual_seed(seed + 100)
+    dout = torch.randn(x.shape, generator=g, device=x.device).to(x.dtype)
+    ref_out, ref_dx, ref_drw, ref_drb, ref_exp, ref_shared = _oracle(layer, x, dout)
+    layer.requires_grad_(True)
+    layer.zero_grad(set_to_none=True)
+    xl = _leaf(x)
+    out = layer(xl)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    dt = x.dtype
+    rtol = 2e-2 if dt == torch.bfloat16 else 1e-5
+    assert torch.allclose(out.detach().float(), ref_out.float(), rtol=rtol, atol=rtol / 10) or \
+        (out.detach().float() - ref_out.float()).abs().max() <= 0.05 * ref_out.float().abs().max()
+    _close(xl.grad, ref_dx, dt, f"{label} dx")
+    _close(layer.router.weight.grad, ref_drw, dt, f"{label} d router.weight")
+    if ref_drb is not None:
+        _close(layer.router.bias.grad, ref_drb, dt, f"{label} d router.bias")
+    n_none = 0
+    for e, (m, r) in enumerate(zip(layer.routed_experts, ref_exp)):
+        for name, got, want in (("gate", m.gate.weight.grad, r.gate.grad), ("up", m.up.weight.grad, r.up.grad),
+                                ("down", m.down.weight.grad, r.down.grad)):
+            if want is None:
+                assert got is None, f"{label}: expert {e} has no rows but got a {name} gradient"
+                n_none += 1
+                continue
+            _close(got, want, dt, f"{label} d expert{e}.{name}")
+    for i, (m, r) in enumerate(zip(layer.shared_experts, ref_shared)):
+        for name, got, want in (("gate", m.gate.weight.grad, r.gate.grad), ("up", m.up.weight.grad, r.up.grad),
+                                ("down", m.down.weight.grad, r.down.grad)):
+            _close(got, want, dt, f"{label} d shared{i}.{name}")
+    return n_none
+
+
+def _random_layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, seed=0, router_scale=1.0, bias=False):
+    torch.manual_seed(seed)
+    layer = DeepSeekMoE(dim, dim_ffn, n_exp, n_shared_experts=n_shared, n_activated_experts=top_k)
+    for m in layer.modules():
+        if hasattr(m, "reset_parameters"):
+            m.reset_parameters()
+    with torch.no_grad():
+        layer.router.weight.mul_(router_scale)
+    if bias:
+        layer.router.bias = torch.nn.Parameter(torch.linspace(-1.0, 1.0, n_exp))
+    return layer.to(device=gpu, dtype=dtype)
+
+
+@pytest.mark.parametrize("dim,dim_ffn,n_exp,n_shared,top_k,dtype,bias", [
+    (64, 128, 8, 0, 2, torch.float32, True),
+    (96, 80, 6, 2, 3, torch.float32, False),
+    (8, 16, 4, 1, 2, torch.bfloat16, False),   # the reference's tiny MoE test config
+    (256, 512, 8, 1, 2, torch.bfloat16, False),
+    (512, 256, 16, 0, 4, torch.bfloat16, True),
+])
+def test_moe_backward(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, bias):
+    layer = _random_layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, bias=bias)
+    g = torch.Generator(device=gpu).manual_seed(3)
+    x = torch.randn(2, 61, dim, generator=g, device=gpu).to(dtype)
+    _check_moe(layer, x, f"d{dim}_f{dim_ffn}_e{n_exp}_s{n_shared}_k{top_k}_{dtype}")
+
+
+def test_moe_backward_empty_experts(gpu):
+    # a sharp router leaves most of the 32 experts without tokens
+    layer = _random_layer(gpu, 128, 256, 32, 0, 2, torch.bfloat16, router_scale=40.0, bias=True)
+    with torch.no_grad():
+        layer.router.bias.copy_(torch.linspace(-30.0, 30.0, 32, device=gpu))
+    x = torch.randn(1, 40, 128, device=gpu).to(torch.bfloat16)
+    n_none = _check_moe(layer, x, "empty experts")
+    assert n_none >= 3 * 10
+
+
+def test_moe_backward_workload_rows(gpu):
+    # the fine-grained workload's weights with 2048 tokens (256-row GEMM tiles)
+    layer, x = make_layer(WORKLOADS["moe_bf16_d2048_f1408_e64_k6_t8192"], gpu, n_tokens=2048)
+    _check_moe(layer, x, "d2048_f1408_e64_k6 t2048")
+
+
+def test_mlp_backward(gpu):
+    torch.manual_seed(1)
+    mlp = MLP(192, 320).to(device=gpu, dtype=torch.bfloat16)
+    for m in mlp.modules():
+        if hasattr(m, "reset_parameters"):
+            m.reset_parameters()
+    x = torch.randn(3, 50, 192, device=gpu).to(torch.bfloat16)
+    dout = torch.randn(3, 50, 192, device=gpu).to(torch.bfloat16)
+    w = R.ExpertWeights(_leaf(mlp.gate.weight), _leaf(mlp.up.weight), _leaf(mlp.down.weight))
+    xr = _leaf(x)
+    R.expert_mlp(xr, w).backward(dout)
+    xl = _leaf(x)
+    mlp(xl).backward(dout)
+    torch.cuda.synchronize()
+    _close(xl.grad, xr.grad, torch.bfloat16, "mlp dx")
+    for name, got, want in (("gate", mlp.gate.weight.grad, w.gate.grad), ("up", mlp.up.weight.grad, w.up.grad),
+                            ("down", mlp.down.weight.grad, w.down.grad)):
+        _close(got, want, torch.bfloat16, f"mlp d{name}")
+
+
+def test_inference_mode_has_no_graph(gpu):
+    layer = _random_layer(gpu, 64, 128, 4, 1, 2, torch.bfloat16)
+    x = torch.randn(1, 8, 64, device=gpu).to(torch.bfloat16)
+    with torch.inference_mode():
+        out = layer(x)
+    assert out.grad_fn is None

@@ -111,11 +111,3 @@ def test_deterministic_repeat(gpu):
         b = layer(x)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
-
-
-def test_grad_mode_raises(gpu):
-    layer = _random_layer(gpu, 64, 128, 4, 0, 2, torch.bfloat16)
-    layer.requires_grad_(True)
-    x = torch.randn(1, 4, 64, device=gpu, dtype=torch.bfloat16)
-    with pytest.raises(NotImplementedError):
-        layer(x)
