@@ -51,6 +51,8 @@ def _parse():
     p.add_argument("--workload", default=None, help="workload name (default: the Mixtral-shaped layer)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU work for the baseline sample")
+    p.add_argument("--graph", action="store_true",
+                   help="also time the step as a replayed HIP graph (reported as graph_*; value stays eager)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="before timing, copy a buffer of this many MiB once (a plain copy kernel of known size "
                         "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -180,6 +182,28 @@ def main():
         logits = layer.router(x.view(-1, w.dim))
         counts = ops.moe_route(logits, w.top_k).chunk_hist.sum(0)
         torch.cuda.synchronize()
+
+        graph_ms = None
+        if args.graph:
+            graph = torch.cuda.CUDAGraph()
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                layer(x)
+                stream.synchronize()
+                with torch.cuda.graph(graph, stream=stream):
+                    layer(x)
+            torch.cuda.current_stream().wait_stream(stream)
+            for _ in range(args.warmup):
+                graph.replay()
+            torch.cuda.synchronize()
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record()
+            for _ in range(args.steps):
+                graph.replay()
+            g1.record()
+            torch.cuda.synchronize()
+            graph_ms = g0.elapsed_time(g1) / args.steps
     assert torch.isfinite(out.float()).all()
 
     bf16 = w.dtype == torch.bfloat16
@@ -230,6 +254,9 @@ def main():
         "expert_weight_stream_gbs": weight_bytes / (t_gu + t_dn) / 1e9,
         "routing": routing_stats(counts),
     }
+    if graph_ms is not None:
+        result["graph_ms_per_step"] = graph_ms
+        result["graph_value"] = T / (graph_ms / 1e3)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(layer, x, w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
