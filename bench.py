@@ -51,6 +51,8 @@ def _parse():
     p.add_argument("--workload", default=None, help="workload name (default: the Mixtral-shaped layer)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU work for the baseline sample")
+    p.add_argument("--backward", action="store_true",
+                   help="also time forward + backward (reported as train_*; value stays the forward)")
     p.add_argument("--graph", action="store_true",
                    help="also time the step as a replayed HIP graph (reported as graph_*; value stays eager)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
@@ -206,6 +208,26 @@ def main():
             graph_ms = g0.elapsed_time(g1) / args.steps
     assert torch.isfinite(out.float()).all()
 
+    train_ms = None
+    if args.backward:
+        layer.requires_grad_(True)
+        xg = x.detach().clone().requires_grad_(True)
+        dout = torch.randn_like(x)
+        for _ in range(max(1, args.warmup // 2)):
+            layer(xg).backward(dout)
+        torch.cuda.synchronize()
+        b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n_train = max(1, args.steps // 2)
+        b0.record()
+        for _ in range(n_train):
+            layer.zero_grad(set_to_none=True)
+            xg.grad = None
+            layer(xg).backward(dout)
+        b1.record()
+        torch.cuda.synchronize()
+        train_ms = b0.elapsed_time(b1) / n_train
+        layer.requires_grad_(False)
+
     bf16 = w.dtype == torch.bfloat16
     s = 2 if bf16 else 4
     peak = PEAK_BF16_TFLOPS if bf16 else PEAK_FP32_TFLOPS
@@ -254,6 +276,9 @@ def main():
         "expert_weight_stream_gbs": weight_bytes / (t_gu + t_dn) / 1e9,
         "routing": routing_stats(counts),
     }
+    if train_ms is not None:
+        result["train_ms_per_step"] = train_ms
+        result["train_value"] = T / (train_ms / 1e3)
     if graph_ms is not None:
         result["graph_ms_per_step"] = graph_ms
         result["graph_value"] = T / (graph_ms / 1e3)

@@ -111,3 +111,26 @@ def test_deterministic_repeat(gpu):
         b = layer(x)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_checkpoint_load_into_live_layer(gpu, tmp_path):
+    # weights loaded in place (load_state_dict) or swapped (new parameters) after the layer has run:
+    # the kernels must see the new weights
+    from safetensors.torch import load_file, save_file
+
+    a = _random_layer(gpu, 128, 256, 8, 1, 2, torch.bfloat16, seed=0)
+    b = _random_layer(gpu, 128, 256, 8, 1, 2, torch.bfloat16, seed=1)
+    x = torch.randn(1, 96, 128, device=gpu).to(torch.bfloat16)
+    with torch.no_grad():
+        a(x)  # builds a's weight-pointer tables
+        path = tmp_path / "b.safetensors"
+        save_file({k: v.cpu() for k, v in b.state_dict().items()}, str(path))
+        a.load_state_dict(load_file(str(path), device=str(gpu)))
+        out_a, out_b = a(x), b(x)
+        assert torch.equal(out_a, out_b)
+        c = _random_layer(gpu, 128, 256, 8, 1, 2, torch.bfloat16, seed=2)
+        for m_a, m_c in zip(a.routed_experts, c.routed_experts):
+            m_a.gate.weight = m_c.gate.weight
+        assert not torch.equal(a(x), out_b)
+        check_layer(a, x, "swapped gate weights")
+

@@ -105,6 +105,22 @@ def test_state_dict_round_trip():
         assert ka == kb and torch.equal(va, vb)
 
 
+def test_safetensors_checkpoint_round_trip(tmp_path):
+    # the reference's checkpoints are safetensors files keyed like the module's state_dict
+    from safetensors.torch import load_file, save_file
+
+    a = DeepSeekMoE(8, 16, 3, n_shared_experts=2)
+    for p in a.parameters():
+        nn.init.normal_(p)
+    path = tmp_path / "moe.safetensors"
+    save_file(a.state_dict(), str(path))
+    b = DeepSeekMoE(8, 16, 3, n_shared_experts=2)
+    missing, unexpected = b.load_state_dict(load_file(str(path)))
+    assert not missing and not unexpected
+    for k, v in a.state_dict().items():
+        assert torch.equal(v, b.state_dict()[k])
+
+
 def test_cpu_input_raises_instead_of_falling_back():
     m = DeepSeekMoE(8, 16, 4, n_shared_experts=0)
     with torch.no_grad(), pytest.raises(RuntimeError, match="ROCm device"):
