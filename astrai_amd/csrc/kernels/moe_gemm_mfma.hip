@@ -265,32 +265,98 @@ __host__ __device__ constexpr int staged_row_bytes() {
 // ===========================================================================
 // Streaming kernel: 256 x 256 tiles, 8 matrix-core waves + 4 DMA waves.
 // ===========================================================================
+template <bool kGateUp>
 struct StreamCfg {
   static constexpr int BM = 256, BN = 256, GM = 8;
   static constexpr int WGM = 2, WGN = 4, MW = 8, DW = 4;  // matrix-core waves (WGM x WGN), DMA waves
   static constexpr int WAVES = MW + DW, THREADS = WAVES * 64;
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // 128 x 64 per matrix-core wave
-  static constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes;
-  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;  // 64 KB, two stages
-  static constexpr int A_OPS = A_BYTES / 1024 / DW;      // 1 KB DMA ops per DMA wave per step
-  static constexpr int B_OPS = B_BYTES / 1024 / DW;
-  static constexpr int AR = 4;  // A-fragment ring slots
-  static constexpr int PD = 2;  // A-fragment prefetch distance (rows of 16)
-  static_assert(STAGE_BYTES == 65536, "stage buffers toggle by xor 65536");
+  static constexpr int A_BYTES = BM * kRowBytes, B_BYTES = BN * kRowBytes;  // 32 KB per 64-K step each
+  static constexpr int A_STAGES = 2, B_STAGES = 3;
+  static constexpr int A_OFF = 0, B_OFF = A_STAGES * A_BYTES;
+  static constexpr int LDS = B_OFF + B_STAGES * B_BYTES;  // 160 KB
+  static constexpr int OPS = A_BYTES / 1024 / DW;         // 1 KB DMA ops per DMA wave per operand and step
+  // A-fragment ring slots and prefetch distance (rows of 16): the largest
+  // that compile without spills in the K loop
+  static constexpr int AR = kGateUp ? 4 : 2;
+  static constexpr int PD = kGateUp ? 2 : 1;
+  static_assert(A_BYTES == B_BYTES && A_BYTES % (1024 * DW) == 0, "one DMA group size");
+  static_assert(A_BYTES == 32768 && A_STAGES == 2, "activation buffers toggle by xor 32768");
+  static_assert(LDS <= 160 * 1024, "LDS");
   static_assert(16 % AR == 0 && PD >= 1 && PD < AR, "the prefetch slot is never the current row's");
-  static_assert((A_OPS + B_OPS) * 2 <= 63, "vmcnt range");
+  static_assert(3 * OPS <= 63, "vmcnt range");
+};
+
+// Epilogue straight from the accumulators: lane l holds 4 consecutive output
+// columns of one row per 16x16 tile, stored as one 8-byte write (rows of a
+// tile are written by 16 lanes at once; L2 merges the pieces of each line).
+template <bool kGateUp, int WM, int WN, int BN>
+__device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 16], const bf16_t* row_w, bf16_t* C,
+                                                  int N, int wm, int wn, int t_row0, int t_rows, int t_nt) {
+  constexpr int MT16 = WM / 16, NT16 = WN / 16;
+  const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int row_l = el & 15;
+  const int col_l = 4 * (el >> 4);
+  const int n_base = kGateUp ? t_nt * (BN / 2) + wn * (WN / 2) : t_nt * BN + wn * WN;
+#pragma unroll
+  for (int i = 0; i < MT16; ++i) {
+    const int gm = wm * WM + i * 16 + row_l;
+    const int srow = t_row0 + min(gm, t_rows - 1);
+    constexpr int NJ = kGateUp ? NT16 / 2 : NT16;
+    float w = 1.0f;
+    if (!kGateUp) w = bf16_bits_to_f32(row_w[srow]);
+    bf16_t* crow = C + (int64_t)srow * N + n_base + col_l;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      bf16x4_t o;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (kGateUp) {
+          const float g = (float)(__bf16)acc[i][j][r];
+          const float u = (float)(__bf16)acc[i][j + NJ][r];
+          const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+          const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
+          o[r] = (__bf16)(u * sv);
+        } else {
+          o[r] = (__bf16)((float)(__bf16)acc[i][j][r] * w);
+        }
+      }
+      if (gm < t_rows) *reinterpret_cast<bf16x4_t*>(crow + j * 16) = o;
+    }
+  }
+}
+
+// Position of a DMA wave in this workgroup's step sequence: the tile and K
+// step it loads next, and that tile's global bases.
+template <int BM, int BN, int GM, bool kGateUp>
+struct StepCursor {
+  int logical, mt, nt, kt;
+  bool live;
+  TileSrc<BM, BN, kGateUp> src;
+  __device__ void start(const TileWalk<GM>& walk, int logical_, int mt_, int nt_, const int32_t* tiles,
+                        const bf16_t* A, const void* const* W0, const void* const* W1, int K) {
+    logical = logical_, mt = mt_, nt = nt_, kt = 0, live = true;
+    (void)walk;
+    src.setup(tiles, A, W0, W1, K, mt, nt);
+  }
+  __device__ void advance(const TileWalk<GM>& walk, const int32_t* tiles, const bf16_t* A, const void* const* W0,
+                          const void* const* W1, int K, int KT) {
+    if (++kt == KT) {
+      kt = 0;
+      logical = walk.seek(logical + walk.G, mt, nt);
+      live = logical < walk.total;
+      if (live) src.setup(tiles, A, W0, W1, K, mt, nt);
+    }
+  }
 };
 
 template <bool kGateUp>
-__global__ __launch_bounds__(StreamCfg::THREADS, 1) void gemm_stream_kernel(
+__global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
     int capacity, bf16_t* __restrict__ C) {
-  using Cfg = StreamCfg;
-  constexpr int STAGE_AREA = 2 * Cfg::STAGE_BYTES;
-  constexpr int OROW = staged_row_bytes<kGateUp, Cfg::WN>();
-  static_assert(STAGE_AREA + Cfg::MW * 16 * OROW <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) char smem[STAGE_AREA + Cfg::MW * 16 * OROW];
+  using Cfg = StreamCfg<kGateUp>;
+  __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
 
   const TileWalk<Cfg::GM> walk(tiles, capacity, n_tiles_n);
   int mt = 0, nt = 0;
@@ -301,60 +367,57 @@ __global__ __launch_bounds__(StreamCfg::THREADS, 1) void gemm_stream_kernel(
   const int lane = threadIdx.x & 63;
   const int KT = K / kBK;  // steps per tile
 
-  // Global steps g = 0, 1, ... run over this workgroup's tiles back to back;
-  // step g lives in buffer g % 2. Barrier X_g: every matrix-core wave has
-  // read all of step g, and step g + 1 has landed. Every wave executes one
-  // X_{-1} and then exactly one X_g per step.
+  // Global steps g = 0, 1, ... run over this workgroup's tiles back to back.
+  // Step g's activations live in A-buffer g % 2 and its weights in B-buffer
+  // g % 3. Barrier X_g: every matrix-core wave has read all of step g, and
+  // A(g + 1) and B(g + 1) have landed; after it the DMA waves load A(g + 2)
+  // and B(g + 3) into the buffers step g held. The weights, which come from
+  // HBM, thus have two steps to land, the activations one. Every wave
+  // executes X_{-1} and then exactly one X_g per step.
   if (wave >= Cfg::MW) {
     // ---------------- DMA waves ----------------
     const int dw = wave - Cfg::MW;
     const uint32_t k2 = (uint32_t)K * 2u;
-    TileSrc<Cfg::BM, Cfg::BN, kGateUp> src;
-    // cursor: the next step to issue
-    int c_logical = logical, c_mt = mt, c_nt = nt, c_kt = 0;
-    bool c_live = true;
-    src.setup(tiles, A, W0, W1, K, c_mt, c_nt);
-    auto issue_next = [&](int buf) {
-      char* sa = smem + buf * Cfg::STAGE_BYTES;
-      char* sb = sa + Cfg::A_BYTES;
-      const DmaLane dl(lane, c_kt);
-      // expert weights first: they come from HBM and take longest to land
+    StepCursor<Cfg::BM, Cfg::BN, Cfg::GM, kGateUp> ca, cb;  // next A step, next B step
+    ca.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
+    cb.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
+    auto issue_a = [&](int buf) {
+      const DmaLane dl(lane, ca.kt);
+      char* base = smem + Cfg::A_OFF + buf * Cfg::A_BYTES;
 #pragma unroll
-      for (int i = 0; i < Cfg::B_OPS; ++i) {
-        const int q = dw * Cfg::B_OPS + i;
-        src.dma_b(dl, q, k2, sb + q * 1024);
+      for (int i = 0; i < Cfg::OPS; ++i) {
+        const int q = dw * Cfg::OPS + i;
+        ca.src.dma_a(dl, q, k2, base + q * 1024);
       }
-#pragma unroll
-      for (int i = 0; i < Cfg::A_OPS; ++i) {
-        const int q = dw * Cfg::A_OPS + i;
-        src.dma_a(dl, q, k2, sa + q * 1024);
-      }
-      if (++c_kt == KT) {
-        c_kt = 0;
-        c_logical = walk.seek(c_logical + walk.G, c_mt, c_nt);
-        c_live = c_logical < walk.total;
-        if (c_live) src.setup(tiles, A, W0, W1, K, c_mt, c_nt);
-      }
+      ca.advance(walk, tiles, A, W0, W1, K, KT);
     };
-    int issued = 1;
-    issue_next(0);
-    if (c_live) {
-      issue_next(1);
-      ++issued;
-      wait_vmcnt<Cfg::A_OPS + Cfg::B_OPS>();  // step 0 landed
-    } else {
-      wait_vmcnt<0>();
-    }
-    __builtin_amdgcn_s_barrier();  // X_{-1}
-    for (int g = 0;; ++g) {
-      wait_vmcnt<0>();               // step g + 1 landed (the only one in flight)
-      __builtin_amdgcn_s_barrier();  // X_g
-      if (c_live) {
-        issue_next(g & 1);  // step g + 2 into step g's buffer
-        ++issued;
-      } else if (g + 1 >= issued) {
-        break;  // X_g was the last step's barrier
+    auto issue_b = [&](int buf) {
+      const DmaLane dl(lane, cb.kt);
+      char* base = smem + Cfg::B_OFF + buf * Cfg::B_BYTES;
+#pragma unroll
+      for (int i = 0; i < Cfg::OPS; ++i) {
+        const int q = dw * Cfg::OPS + i;
+        cb.src.dma_b(dl, q, k2, base + q * 1024);
       }
+      cb.advance(walk, tiles, A, W0, W1, K, KT);
+    };
+    // prologue in issue order B0, A0, B1, A1, B2 (as far as the steps exist)
+    int a_iss = 0, b_iss = 0;
+    issue_b(0), ++b_iss;
+    issue_a(0), ++a_iss;
+    if (cb.live) issue_b(1), ++b_iss;
+    if (ca.live) issue_a(1), ++a_iss;
+    if (cb.live) issue_b(2), ++b_iss;
+    wait_groups<Cfg::OPS, 3>((a_iss - 1) + (b_iss - 1));  // A0 and B0 landed
+    __builtin_amdgcn_s_barrier();                          // X_{-1}
+    for (int g = 0;; ++g) {
+      // A(g + 1) and B(g + 1) landed; B(g + 2), issued after A(g + 1), may stay in flight
+      wait_groups<Cfg::OPS, 1>(b_iss > g + 2 ? 1 : 0);
+      __builtin_amdgcn_s_barrier();  // X_g
+      const bool more = ca.live;
+      if (ca.live) issue_a(g & 1), ++a_iss;  // A(g + 2)
+      if (cb.live) issue_b(g % 3), ++b_iss;  // B(g + 3)
+      if (!more && g + 1 >= a_iss) break;    // X_g was the last step's barrier
     }
     return;
   }
@@ -366,36 +429,41 @@ __global__ __launch_bounds__(StreamCfg::THREADS, 1) void gemm_stream_kernel(
   constexpr int AR = Cfg::AR, PD = Cfg::PD;
   const int frag_row = lane & 15;
   const int fq = lane >> 4;
-  // LDS byte addresses of the lane's fragments: the second 32-K half is the
-  // first with chunk bit 2 flipped (xor 64), buffer 1 is buffer 0 xor 65536,
-  // and row / column block offsets are immediates.
+  // LDS byte addresses of the lane's fragments in the current buffers: the
+  // second 32-K half is the first with chunk bit 2 flipped (xor 64); row and
+  // column block offsets are immediates.
   const uint32_t v_lane = frag_row * kRowBytes + ((fq ^ ((frag_row >> 1) & 7)) << 4);
   const uint32_t b_row = kGateUp ? wn * (Cfg::WN / 2) : wn * Cfg::WN;
-  uint32_t vA = (uint32_t)(wm * Cfg::WM) * kRowBytes + v_lane;
-  uint32_t vB = (uint32_t)Cfg::A_BYTES + b_row * kRowBytes + v_lane;
-  auto toggle = [&]() {
-    vA ^= 65536u;
-    vB ^= 65536u;
+  uint32_t vA = (uint32_t)Cfg::A_OFF + (uint32_t)(wm * Cfg::WM) * kRowBytes + v_lane;
+  uint32_t vB = (uint32_t)Cfg::B_OFF + b_row * kRowBytes + v_lane;
+  constexpr uint32_t kBEnd = (uint32_t)Cfg::LDS;
+  auto next_b = [&](uint32_t v) -> uint32_t {
+    const uint32_t n = v + Cfg::B_BYTES;
+    return n >= kBEnd ? n - Cfg::B_STAGES * Cfg::B_BYTES : n;
+  };
+  auto rotate = [&]() {
+    vA ^= (uint32_t)Cfg::A_BYTES;
+    vB = next_b(vB);
     asm volatile("" : "+v"(vA), "+v"(vB));
   };
   bf16x8_t fa[AR], fb[NT16];
   f32x4_t acc[MT16][NT16];
   auto lds128 = [&](uint32_t addr) -> bf16x8_t { return *reinterpret_cast<const bf16x8_t*>(smem + addr); };
-  auto rdA = [&](bool other, int kh, int i) -> bf16x8_t {
-    return lds128((vA ^ ((other ? 65536u : 0u) | (kh ? 64u : 0u))) + i * 16 * kRowBytes);
+  auto rdA = [&](uint32_t base, int kh, int i) -> bf16x8_t {
+    return lds128((base ^ (kh ? 64u : 0u)) + i * 16 * kRowBytes);
   };
-  auto rdB = [&](bool other, int kh, int j) -> bf16x8_t {
+  auto rdB = [&](uint32_t base, int kh, int j) -> bf16x8_t {
     constexpr int half = NT16 / 2;
     const int r = kGateUp ? ((j < half) ? j * 16 : Cfg::BN / 2 + (j - half) * 16) : j * 16;
-    return lds128((vB ^ ((other ? 65536u : 0u) | (kh ? 64u : 0u))) + r * kRowBytes);
+    return lds128((base ^ (kh ? 64u : 0u)) + r * kRowBytes);
   };
   // one 64-K step as 16 rows of 16 (two 32-K halves x 8 row blocks), 4 MFMAs
   // each; A rows are prefetched PD rows ahead into the ring; B fragments of
   // the next half are reloaded right after their last use; X_g sits before
-  // the first read that targets the next step (from the other buffer, only if
-  // kNext).
+  // the first read that targets the next step (only if kNext).
   auto step = [&](auto next_c) {
     constexpr bool kNext = decltype(next_c)::value;
+    uint32_t nA = 0, nB = 0;
     static_for<16>([&](auto rr) {
       constexpr int r = decltype(rr)::value;
       constexpr int i = r % 8;
@@ -404,17 +472,21 @@ __global__ __launch_bounds__(StreamCfg::THREADS, 1) void gemm_stream_kernel(
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();  // X_g
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kNext) {
+          nA = vA ^ (uint32_t)Cfg::A_BYTES;
+          nB = next_b(vB);
+        }
       }
       if constexpr (rp < 16) {
-        fa[rp % AR] = rdA(false, rp / 8, rp % 8);
+        fa[rp % AR] = rdA(vA, rp / 8, rp % 8);
       } else if constexpr (kNext) {
-        fa[rp % AR] = rdA(true, 0, rp - 16);
+        fa[rp % AR] = rdA(nA, 0, rp - 16);
       }
 #pragma unroll
       for (int j = 0; j < NT16; ++j) {
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[r % AR], acc[i][j], 0, 0, 0);
-        if constexpr (r == 7) fb[j] = rdB(false, 1, j);
-        if constexpr (r == 15 && kNext) fb[j] = rdB(true, 0, j);
+        if constexpr (r == 7) fb[j] = rdB(vB, 1, j);
+        if constexpr (r == 15 && kNext) fb[j] = rdB(nB, 0, j);
       }
       // a tile's last step keeps source order: scheduled freely, its reads
       // move up and the epilogue that follows runs out of registers
@@ -423,7 +495,6 @@ __global__ __launch_bounds__(StreamCfg::THREADS, 1) void gemm_stream_kernel(
   };
 
   lds_barrier();  // X_{-1}
-  char* stage = smem + STAGE_AREA + wave * (16 * OROW);
   while (true) {
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int t_row0 = ti[1];
@@ -436,17 +507,17 @@ __global__ __launch_bounds__(StreamCfg::THREADS, 1) void gemm_stream_kernel(
         for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
     // the step's first fragments: B of the first half and A rows 0..PD-1
 #pragma unroll
-    for (int j = 0; j < NT16; ++j) fb[j] = rdB(false, 0, j);
+    for (int j = 0; j < NT16; ++j) fb[j] = rdB(vB, 0, j);
 #pragma unroll
-    for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(false, 0, r);
+    for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
     for (int kt = 0; kt + 1 < KT; ++kt) {
       step(std::true_type{});
-      toggle();
+      rotate();
     }
     step(std::false_type{});
-    toggle();
+    rotate();
     __builtin_amdgcn_sched_barrier(0);
-    store_tile<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN>(acc, stage, row_w, C, N, wm, wn, t_row0, t_rows, nt);
+    store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt);
     logical = walk.seek(logical + walk.G, mt, nt);
     if (logical >= walk.total) break;
   }
@@ -625,7 +696,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
 // Decode tiles: 32 x 256 outputs, 4 waves of 32 x 64, four stages in flight
 // to keep the expert-weight stream busy; every wave issues DMA.
 using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8>;
-static_assert(StreamCfg::BM == kMfmaBigBM, "prefill tile height");
+static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfmaBigBM, "prefill tile height");
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
@@ -656,10 +727,11 @@ template <bool kGateUp>
 int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
                   const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s) {
   if (capacity == 0) return ASTRAI_MOE_OK;
-  const int64_t n_tiles_n = kGateUp ? N / (StreamCfg::BN / 2) : N / StreamCfg::BN;
+  using Cfg = StreamCfg<kGateUp>;
+  const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp>), dim3((unsigned)grid), dim3(StreamCfg::THREADS), 0, s,
+  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
                      static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
                      (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C));
   return check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>");
