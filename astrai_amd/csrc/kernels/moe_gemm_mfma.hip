@@ -276,14 +276,14 @@ struct StreamCfg {
   static constexpr int A_OFF = 0, B_OFF = A_STAGES * A_BYTES;
   static constexpr int LDS = B_OFF + B_STAGES * B_BYTES;  // 160 KB
   static constexpr int OPS = A_BYTES / 1024 / DW;         // 1 KB DMA ops per DMA wave per operand and step
-  // A-fragment ring slots and prefetch distance (rows of 16): the largest
-  // that compile without spills in the K loop
-  static constexpr int AR = kGateUp ? 4 : 2;
-  static constexpr int PD = kGateUp ? 2 : 1;
+  // Rows of 16 are taken in pairs, columns outer within a pair, so each B
+  // fragment reloaded after its last use in a half has 6 MFMAs of lead; A
+  // fragments stream through a ring of AR slots PD rows ahead.
+  static constexpr int RG = 2, AR = 4, PD = 2;
   static_assert(A_BYTES == B_BYTES && A_BYTES % (1024 * DW) == 0, "one DMA group size");
   static_assert(A_BYTES == 32768 && A_STAGES == 2, "activation buffers toggle by xor 32768");
   static_assert(LDS <= 160 * 1024, "LDS");
-  static_assert(16 % AR == 0 && PD >= 1 && PD < AR, "the prefetch slot is never the current row's");
+  static_assert(16 % AR == 0 && 8 % RG == 0 && PD >= RG && PD + RG <= AR, "ring slots of a pair and its prefetch");
   static_assert(3 * OPS <= 63, "vmcnt range");
 };
 
@@ -457,18 +457,18 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     const int r = kGateUp ? ((j < half) ? j * 16 : Cfg::BN / 2 + (j - half) * 16) : j * 16;
     return lds128((base ^ (kh ? 64u : 0u)) + r * kRowBytes);
   };
-  // one 64-K step as 16 rows of 16 (two 32-K halves x 8 row blocks), 4 MFMAs
-  // each; A rows are prefetched PD rows ahead into the ring; B fragments of
-  // the next half are reloaded right after their last use; X_g sits before
-  // the first read that targets the next step (only if kNext).
+  // one 64-K step as 16 rows of 16 (two 32-K halves x 8 row blocks) taken in
+  // groups of RG rows, 4 x RG MFMAs each; A rows are prefetched PD rows ahead
+  // into the ring; B fragments of the next half are reloaded right after
+  // their last use; X_g sits before the first read that targets the next
+  // step (only if kNext).
+  constexpr int RG = Cfg::RG;
   auto step = [&](auto next_c) {
     constexpr bool kNext = decltype(next_c)::value;
     uint32_t nA = 0, nB = 0;
-    static_for<16>([&](auto rr) {
-      constexpr int r = decltype(rr)::value;
-      constexpr int i = r % 8;
-      constexpr int rp = r + PD;
-      if constexpr (rp == 16) {
+    static_for<16 / RG>([&](auto gg) {
+      constexpr int r0 = decltype(gg)::value * RG;
+      if constexpr (r0 + PD >= 16 && r0 + PD < 16 + RG) {
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();  // X_g
         __builtin_amdgcn_sched_barrier(0);
@@ -477,16 +477,22 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
           nB = next_b(vB);
         }
       }
-      if constexpr (rp < 16) {
-        fa[rp % AR] = rdA(vA, rp / 8, rp % 8);
-      } else if constexpr (kNext) {
-        fa[rp % AR] = rdA(nA, 0, rp - 16);
-      }
+      static_for<RG>([&](auto qq) {
+        constexpr int rp = r0 + PD + decltype(qq)::value;
+        if constexpr (rp < 16) {
+          fa[rp % AR] = rdA(vA, rp / 8, rp % 8);
+        } else if constexpr (kNext) {
+          fa[rp % AR] = rdA(nA, 0, rp - 16);
+        }
+      });
 #pragma unroll
       for (int j = 0; j < NT16; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[r % AR], acc[i][j], 0, 0, 0);
-        if constexpr (r == 7) fb[j] = rdB(vB, 1, j);
-        if constexpr (r == 15 && kNext) fb[j] = rdB(nB, 0, j);
+        static_for<RG>([&](auto qq) {
+          constexpr int r = r0 + decltype(qq)::value;
+          acc[r % 8][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[r % AR], acc[r % 8][j], 0, 0, 0);
+        });
+        if constexpr (r0 + RG == 8) fb[j] = rdB(vB, 1, j);
+        if constexpr (r0 + RG == 16 && kNext) fb[j] = rdB(nB, 0, j);
       }
       // a tile's last step keeps source order: scheduled freely, its reads
       // move up and the epilogue that follows runs out of registers
