@@ -501,6 +501,11 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
   };
 
   lds_barrier();  // X_{-1}
+  // the first step's first fragments: B of the first half and A rows 0..PD-1
+#pragma unroll
+  for (int j = 0; j < NT16; ++j) fb[j] = rdB(vB, 0, j);
+#pragma unroll
+  for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
   while (true) {
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int t_row0 = ti[1];
@@ -511,17 +516,15 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
       for (int j = 0; j < NT16; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
-    // the step's first fragments: B of the first half and A rows 0..PD-1
-#pragma unroll
-    for (int j = 0; j < NT16; ++j) fb[j] = rdB(vB, 0, j);
-#pragma unroll
-    for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
-    for (int kt = 0; kt + 1 < KT; ++kt) {
+    // Every step, a tile's last included, prefetches the first fragments of
+    // the step after it, which is the next tile's first step (its data has
+    // landed by X_g; after the workgroup's last step the reads return stale
+    // LDS contents that nothing uses). One loop body keeps one register
+    // assignment, so the accumulators do not spill at tile boundaries.
+    for (int kt = 0; kt < KT; ++kt) {
       step(std::true_type{});
       rotate();
     }
-    step(std::false_type{});
-    rotate();
     __builtin_amdgcn_sched_barrier(0);
     store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt);
     logical = walk.seek(logical + walk.G, mt, nt);
