@@ -16,9 +16,14 @@
 // rounding after every add, then added to the shared output. Results are
 // bit-identical to the reference's sequence of bf16/fp32 adds.
 //
-// One wave per (token, column segment); lanes stream the segment with 16-byte
-// vectors. Rows are split into segments only when there are too few tokens to
-// keep the GPU busy (decode); otherwise a wave takes the whole row.
+// One wave per (token, column segment); lanes stream the segment in 16-byte
+// vectors, U vectors per lane per pass with every row's loads issued before
+// the adds (more bytes in flight per wave: +15-30 % over one vector per pass).
+// Rows are split into segments only when there are too few tokens to keep the
+// GPU busy (decode); otherwise a wave takes the whole row. KMAX bounds top_k
+// at compile time so the row table stays in a few registers; at top-2 the
+// rows are read and the output written with non-temporal hints (each byte is
+// touched once), which measured faster there and slower at top-6.
 #include "moe_common.h"
 
 namespace astrai_moe {
@@ -28,7 +33,37 @@ constexpr int kCombineThreads = 256;
 constexpr int kWavesPerBlock = kCombineThreads / 64;
 constexpr int64_t kTargetWaves = 4096;
 
-template <typename T, int VW>
+template <int VW, typename T>
+struct Vec {  // VW elements of T as one load / store unit
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  static constexpr bool kWide = VW * sizeof(T) == 16;
+  T v[VW];
+  template <bool NT>
+  __device__ void load(const T* p) {
+    if constexpr (kWide) {
+      const u32x4* q = reinterpret_cast<const u32x4*>(p);
+      *reinterpret_cast<u32x4*>(v) = NT ? __builtin_nontemporal_load(q) : *q;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) v[j] = p[j];
+    }
+  }
+  template <bool NT>
+  __device__ void store(T* p) const {
+    if constexpr (kWide) {
+      u32x4* q = reinterpret_cast<u32x4*>(p);
+      if (NT)
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(v), q);
+      else
+        *q = *reinterpret_cast<const u32x4*>(v);
+    } else {
+#pragma unroll
+      for (int j = 0; j < VW; ++j) p[j] = v[j];
+    }
+  }
+};
+
+template <typename T, int VW, int KMAX, int U, bool NT>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
     const T* __restrict__ y, const int32_t* __restrict__ token_pos,
     const T* __restrict__ shared, int n_shared, float inv_shared,
@@ -49,9 +84,10 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
     const int o = __shfl(my_pos, k, 64);
     rank += (o < my_pos) ? 1 : 0;
   }
-  int rows[ASTRAI_MOE_MAX_TOPK];
+  int rows[KMAX];
 #pragma unroll
-  for (int r = 0; r < ASTRAI_MOE_MAX_TOPK; ++r) {
+  for (int r = 0; r < KMAX; ++r) {
+    rows[r] = -1;
     if (r < top_k) {
       // m is wave-uniform; duplicate positions leave some rank unclaimed.
       const uint64_t m = __ballot(lane < top_k && rank == r);
@@ -62,46 +98,67 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
   }
 
   const int64_t v_end = min(nvec, (seg + 1) * seg_units);
-  for (int64_t v = seg * seg_units + lane; v < v_end; v += 64) {
-    float acc[VW];
+  for (int64_t v0 = seg * seg_units + lane; v0 < v_end; v0 += 64 * U) {
+    Vec<VW, T> in[KMAX][U];
 #pragma unroll
-    for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
+    for (int r = 0; r < KMAX; ++r)
+      if (rows[r] >= 0)
 #pragma unroll
-    for (int r = 0; r < ASTRAI_MOE_MAX_TOPK; ++r) {
-      if (r < top_k && rows[r] >= 0) {
-        const T* src = y + (int64_t)rows[r] * dim + v * VW;
-        T vals[VW];
-        if (VW * sizeof(T) == 16)
-          *reinterpret_cast<uint4*>(vals) = *reinterpret_cast<const uint4*>(src);
-        else
+        for (int u = 0; u < U; ++u)
+          if (v0 + u * 64 < v_end) in[r][u].template load<NT>(y + (int64_t)rows[r] * dim + (v0 + u * 64) * VW);
 #pragma unroll
-          for (int j = 0; j < VW; ++j) vals[j] = src[j];
+    for (int u = 0; u < U; ++u) {
+      const int64_t v = v0 + u * 64;
+      if (v >= v_end) break;
+      float acc[VW];
 #pragma unroll
-        for (int j = 0; j < VW; ++j)
-          acc[j] = Elem<T>::round(acc[j] + Elem<T>::to_f32(vals[j]));
+      for (int j = 0; j < VW; ++j) acc[j] = 0.0f;
+#pragma unroll
+      for (int r = 0; r < KMAX; ++r)
+        if (rows[r] >= 0)
+#pragma unroll
+          for (int j = 0; j < VW; ++j) acc[j] = Elem<T>::round(acc[j] + Elem<T>::to_f32(in[r][u].v[j]));
+      float sh[VW];
+#pragma unroll
+      for (int j = 0; j < VW; ++j) sh[j] = 0.0f;
+      for (int si = 0; si < n_shared; ++si) {
+        Vec<VW, T> s_in;
+        s_in.template load<false>(shared + ((int64_t)si * n_tokens + t) * dim + v * VW);
+#pragma unroll
+        for (int j = 0; j < VW; ++j) sh[j] = Elem<T>::round(sh[j] + Elem<T>::to_f32(s_in.v[j]));
       }
+      if (n_shared > 0)
+#pragma unroll
+        for (int j = 0; j < VW; ++j) sh[j] = Elem<T>::round(sh[j] * inv_shared);
+      Vec<VW, T> res;
+#pragma unroll
+      for (int j = 0; j < VW; ++j) res.v[j] = Elem<T>::from_f32(sh[j] + acc[j]);
+      res.template store<NT>(out + t * dim + v * VW);
     }
-    float sh[VW];
-#pragma unroll
-    for (int j = 0; j < VW; ++j) sh[j] = 0.0f;
-    for (int si = 0; si < n_shared; ++si) {
-      const T* sp = shared + ((int64_t)si * n_tokens + t) * dim + v * VW;
-#pragma unroll
-      for (int j = 0; j < VW; ++j) sh[j] = Elem<T>::round(sh[j] + Elem<T>::to_f32(sp[j]));
-    }
-    if (n_shared > 0)
-#pragma unroll
-      for (int j = 0; j < VW; ++j) sh[j] = Elem<T>::round(sh[j] * inv_shared);
-    T res[VW];
-#pragma unroll
-    for (int j = 0; j < VW; ++j) res[j] = Elem<T>::from_f32(sh[j] + acc[j]);
-    T* dst = out + t * dim + v * VW;
-    if (VW * sizeof(T) == 16)
-      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(res);
-    else
-#pragma unroll
-      for (int j = 0; j < VW; ++j) dst[j] = res[j];
   }
+}
+
+template <typename T, int VW, int KMAX, int U, bool NT>
+void launch_combine_cfg(const void* y, const int32_t* token_pos, const void* shared, int n_shared, float inv_shared,
+                        int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid, void* out,
+                        hipStream_t s) {
+  hipLaunchKernelGGL((combine_kernel<T, VW, KMAX, U, NT>), dim3((unsigned)grid), dim3(kCombineThreads), 0, s,
+                     static_cast<const T*>(y), token_pos, static_cast<const T*>(shared), n_shared, inv_shared,
+                     n_tokens, top_k, dim, seg_units, static_cast<T*>(out));
+}
+
+template <typename T, int VW>
+void dispatch_k(const void* y, const int32_t* token_pos, const void* shared, int n_shared, float inv_shared,
+                int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid, void* out, hipStream_t s) {
+  if (top_k <= 2)
+    launch_combine_cfg<T, VW, 2, 2, true>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units,
+                                          grid, out, s);
+  else if (top_k <= 8)
+    launch_combine_cfg<T, VW, 8, 2, false>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim,
+                                           seg_units, grid, out, s);
+  else
+    launch_combine_cfg<T, VW, ASTRAI_MOE_MAX_TOPK, 1, false>(y, token_pos, shared, n_shared, inv_shared, n_tokens,
+                                                            top_k, dim, seg_units, grid, out, s);
 }
 
 template <typename T>
@@ -123,15 +180,9 @@ int launch_combine(const void* y, const int32_t* token_pos, const void* shared,
   const int64_t grid = ceil_div(waves, kWavesPerBlock);
   if (grid >= (1ll << 31)) return fail(ASTRAI_MOE_EINVAL, "combine: too many tokens");
   if (vec)
-    hipLaunchKernelGGL((combine_kernel<T, kVW>), dim3((unsigned)grid), dim3(kCombineThreads),
-                       0, s, static_cast<const T*>(y), token_pos,
-                       static_cast<const T*>(shared), n_shared, inv_shared,
-                       n_tokens, top_k, dim, seg_units, static_cast<T*>(out));
+    dispatch_k<T, kVW>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units, grid, out, s);
   else
-    hipLaunchKernelGGL((combine_kernel<T, 1>), dim3((unsigned)grid), dim3(kCombineThreads),
-                       0, s, static_cast<const T*>(y), token_pos,
-                       static_cast<const T*>(shared), n_shared, inv_shared,
-                       n_tokens, top_k, dim, seg_units, static_cast<T*>(out));
+    dispatch_k<T, 1>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units, grid, out, s);
   return check_launch("combine_kernel");
 }
 
