@@ -139,6 +139,9 @@ GEMM_CASES = [
     (64, 128, 8, 4096, 1536, torch.bfloat16),
     (300, 16, 4, 512, 256, torch.bfloat16),
     (257, 6, 2, 72, 40, torch.bfloat16),
+    # one 64-K step per tile, several tiles per workgroup: every step is a
+    # tile's last and prefetches the next tile's first fragments
+    (16384, 4, 2, 64, 1024, torch.bfloat16),
     (1024, 8, 2, 512, 1024, torch.float32),
     (100, 5, 3, 36, 20, torch.float32),
 ]
@@ -178,6 +181,9 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
     (100, 8, 3, 40, 2, torch.bfloat16),
     (64, 4, 4, 64, 3, torch.float32),
     (77, 8, 8, 24, 1, torch.bfloat16),
+    (300, 16, 12, 256, 0, torch.bfloat16),  # top_k above 8
+    (200, 4, 1, 128, 0, torch.bfloat16),
+    (90, 32, 20, 64, 1, torch.float32),
 ])
 def test_combine_bit_exact(gpu, n_tok, n_exp, top_k, dim, n_shared, dtype):
     route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=11)
