@@ -20,13 +20,20 @@ bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m,
 bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m,
                          const void* a, const void* c);
 
+// `packed`: the weight tables point at packed copies written by launch_pack
+// (bf16, 256-row tiles of K / 64 contiguous 32 KB blocks in staged order).
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles,
                         int64_t capacity, const void* const* w_gate,
                         const void* const* w_up, int64_t dim, int64_t dim_ffn,
-                        int block_m, void* h, hipStream_t s);
+                        int block_m, bool packed, void* h, hipStream_t s);
 int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
                      const void* const* w_down, const void* sorted_w,
-                     int64_t dim_ffn, int64_t dim, int block_m, void* y,
-                     hipStream_t s);
+                     int64_t dim_ffn, int64_t dim, int block_m, bool packed,
+                     void* y, hipStream_t s);
+
+// Packs one expert's weight for the packed GEMMs: gate/up (w0 = gate, w1 =
+// up, each [rows, k]) or down (w0 = [rows, k]).
+int launch_pack(const void* w0, const void* w1, int64_t rows, int64_t k,
+                bool gate_up, void* out, hipStream_t s);
 
 }  // namespace astrai_moe

@@ -177,7 +177,7 @@ extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
   if (dtype == ASTRAI_MOE_BF16) {
     if (mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h))
       return launch_mfma_gate_up(x_perm, tiles, capacity, w_gate, w_up, dim,
-                                 dim_ffn, block_m, h, s);
+                                 dim_ffn, block_m, false, h, s);
     return launch_generic<bf16_t, true>(x_perm, tiles, capacity, w_gate, w_up,
                                         nullptr, dim, dim_ffn, h, s);
   }
@@ -203,10 +203,76 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
   if (dtype == ASTRAI_MOE_BF16) {
     if (mfma_down_supported(dim_ffn, dim, block_m, h, y))
       return launch_mfma_down(h, tiles, capacity, w_down, sorted_w, dim_ffn,
-                              dim, block_m, y, s);
+                              dim, block_m, false, y, s);
     return launch_generic<bf16_t, false>(h, tiles, capacity, w_down, nullptr,
                                          sorted_w, dim_ffn, dim, y, s);
   }
   return launch_generic<float, false>(h, tiles, capacity, w_down, nullptr,
                                       sorted_w, dim_ffn, dim, y, s);
+}
+
+static bool aligned16_ptr(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+extern "C" int astrai_moe_pack_gate_up(const void* w_gate, const void* w_up,
+                                       int dtype, int64_t dim_ffn, int64_t dim,
+                                       void* packed, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "pack_gate_up: packed weights are bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(dim_ffn > 0 && dim > 0 && dim_ffn % 128 == 0 && dim % 64 == 0 && dim <= (1ll << 22),
+                 "pack_gate_up: needs dim_ffn %% 128 == 0 and dim %% 64 == 0 (got %lld, %lld)",
+                 (long long)dim_ffn, (long long)dim);
+  ASTRAI_REQUIRE(w_gate && w_up && packed, "pack_gate_up: null buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(w_gate) && aligned16_ptr(w_up) && aligned16_ptr(packed),
+                 "pack_gate_up: buffers must be 16-byte aligned");
+  return launch_pack(w_gate, w_up, dim_ffn, dim, true, packed, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_pack_down(const void* w_down, int dtype, int64_t dim,
+                                    int64_t dim_ffn, void* packed, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "pack_down: packed weights are bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(dim > 0 && dim_ffn > 0 && dim % 256 == 0 && dim_ffn % 64 == 0 && dim_ffn <= (1ll << 22),
+                 "pack_down: needs dim %% 256 == 0 and dim_ffn %% 64 == 0 (got %lld, %lld)", (long long)dim,
+                 (long long)dim_ffn);
+  ASTRAI_REQUIRE(w_down && packed, "pack_down: null buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(w_down) && aligned16_ptr(packed), "pack_down: buffers must be 16-byte aligned");
+  return launch_pack(w_down, w_down, dim, dim_ffn, false, packed, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t* tiles, int64_t tiles_len,
+                                              const void* const* w_packed, int dtype, int64_t n_rows,
+                                              int n_experts, int64_t dim, int64_t dim_ffn, int block_m, void* h,
+                                              void* stream) {
+  clear_error();
+  int rc = check_common("gemm_gate_up_packed", x_perm, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn,
+                        block_m, h);
+  if (rc) return rc;
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_gate_up_packed: packed weights are bf16 only");
+  ASTRAI_REQUIRE(n_rows == 0 || mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h),
+                 "gemm_gate_up_packed: unsupported shape (dim %lld, dim_ffn %lld, block_m %d) or alignment",
+                 (long long)dim, (long long)dim_ffn, block_m);
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_packed, "gemm_gate_up_packed: null weight table");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  return launch_mfma_gate_up(x_perm, tiles, capacity, w_packed, w_packed, dim, dim_ffn, block_m, true, h,
+                             static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, int64_t tiles_len,
+                                           const void* const* w_packed, const void* sorted_w, int dtype,
+                                           int64_t n_rows, int n_experts, int64_t dim_ffn, int64_t dim,
+                                           int block_m, void* y, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_down_packed", h, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m,
+                        y);
+  if (rc) return rc;
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_down_packed: packed weights are bf16 only");
+  ASTRAI_REQUIRE(n_rows == 0 || mfma_down_supported(dim_ffn, dim, block_m, h, y),
+                 "gemm_down_packed: unsupported shape (dim_ffn %lld, dim %lld, block_m %d) or alignment",
+                 (long long)dim_ffn, (long long)dim, block_m);
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_packed && sorted_w, "gemm_down_packed: null weight table or row weights");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  return launch_mfma_down(h, tiles, capacity, w_packed, sorted_w, dim_ffn, dim, block_m, true, y,
+                          static_cast<hipStream_t>(stream));
 }

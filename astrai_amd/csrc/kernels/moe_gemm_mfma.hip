@@ -168,8 +168,12 @@ struct DmaLane {
   }
 };
 
-// Per-tile global bases: activation rows and the expert's weight rows.
-template <int BM, int BN, bool kGateUp>
+// Per-tile global bases: activation rows and the expert's weight rows. With
+// kPacked the expert's weight comes as a packed copy (pack_kernel): the BN
+// weight rows of column tile nt are K / 64 contiguous blocks of BN x 128
+// bytes, each already in the staged (swizzled) LDS order, so a step's weight
+// load is one contiguous block.
+template <int BM, int BN, bool kGateUp, bool kPacked = false>
 struct TileSrc {
   const char* a_base = nullptr;
   const char* b_base0 = nullptr;
@@ -182,24 +186,61 @@ struct TileSrc {
     row0 = ti[1];
     rows = min(BM, ti[2] - row0);
     a_base = reinterpret_cast<const char*>(A + (int64_t)row0 * K);
-    b_base0 = reinterpret_cast<const char*>(static_cast<const bf16_t*>(W0[e]) +
-                                            (int64_t)nt * (kGateUp ? BN / 2 : BN) * K);
-    b_base1 = kGateUp ? reinterpret_cast<const char*>(static_cast<const bf16_t*>(W1[e]) + (int64_t)nt * (BN / 2) * K)
-                      : b_base0;
+    if constexpr (kPacked) {
+      b_base0 = static_cast<const char*>(W0[e]) + (int64_t)nt * (K / kBK) * (BN * kRowBytes);
+      b_base1 = b_base0;
+    } else {
+      b_base0 = reinterpret_cast<const char*>(static_cast<const bf16_t*>(W0[e]) +
+                                              (int64_t)nt * (kGateUp ? BN / 2 : BN) * K);
+      b_base1 = kGateUp ? reinterpret_cast<const char*>(static_cast<const bf16_t*>(W1[e]) + (int64_t)nt * (BN / 2) * K)
+                        : b_base0;
+    }
   }
   // 8-row group q of the A tile (pad rows past the tile's last row re-read that row)
   __device__ void dma_a(const DmaLane& dl, int q, uint32_t k2, char* lds) const {
     const uint32_t row = (uint32_t)min(q * 8 + dl.row, rows - 1);
     lds_dma_16(a_base + (row * k2 + dl.chunk(q)), lds);
   }
-  // 8-row group q of the B tile (up rows follow the gate rows)
-  __device__ void dma_b(const DmaLane& dl, int q, uint32_t k2, char* lds) const {
-    const int r0 = q * 8;
-    const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
-    const int rq = (kGateUp && r0 >= BN / 2) ? r0 - BN / 2 : r0;
-    lds_dma_16(bb + ((uint32_t)(rq + dl.row) * k2 + dl.chunk(q)), lds);
+  // 8-row group q of the B tile of K step kstep (up rows follow the gate rows)
+  __device__ void dma_b(const DmaLane& dl, int lane, int kstep, int q, uint32_t k2, char* lds) const {
+    if constexpr (kPacked) {
+      lds_dma_16(b_base0 + ((uint32_t)kstep * (BN * kRowBytes) + (uint32_t)q * 1024 + (uint32_t)lane * 16), lds);
+    } else {
+      (void)lane, (void)kstep;
+      const int r0 = q * 8;
+      const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
+      const int rq = (kGateUp && r0 >= BN / 2) ? r0 - BN / 2 : r0;
+      lds_dma_16(bb + ((uint32_t)(rq + dl.row) * k2 + dl.chunk(q)), lds);
+    }
   }
 };
+
+// Packs one expert's weight for kPacked kernels: for every column tile of BN
+// = 256 weight rows (gate/up: 128 gate rows, then the same 128 up rows) and
+// every 64-K step, the 256 x 128-byte block in staged order: row r's 16-byte
+// chunk c at chunk c ^ ((r >> 1) & 7), as the DMA would have placed it. One
+// thread per 16-byte unit.
+template <bool kGateUp>
+__global__ __launch_bounds__(256) void pack_kernel(const bf16_t* __restrict__ w0, const bf16_t* __restrict__ w1,
+                                                   int64_t n_tiles, int K, uint4* __restrict__ out) {
+  constexpr int BN = 256;
+  const int KT = K / kBK;
+  const int64_t units = n_tiles * KT * BN * 8;
+  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x) {
+    const int p = (int)(u & 7);
+    const int r = (int)((u >> 3) & (BN - 1));
+    const int64_t tk = u >> 11;  // (tile, step)
+    const int kt = (int)(tk % KT);
+    const int64_t nt = tk / KT;
+    const int c = p ^ ((r >> 1) & 7);
+    const bf16_t* row;
+    if (kGateUp)
+      row = (r < BN / 2) ? w0 + (nt * (BN / 2) + r) * (int64_t)K : w1 + (nt * (BN / 2) + r - BN / 2) * (int64_t)K;
+    else
+      row = w0 + (nt * BN + r) * (int64_t)K;
+    out[u] = *reinterpret_cast<const uint4*>(row + kt * kBK + c * 8);
+  }
+}
 
 // Epilogue of one wave's WM x WN accumulator block: bf16 rounding, SiLU * up
 // (gate/up) or * routing weight (down), staged per 16 rows in the wave's own
@@ -328,11 +369,11 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
 
 // Position of a DMA wave in this workgroup's step sequence: the tile and K
 // step it loads next, and that tile's global bases.
-template <int BM, int BN, int GM, bool kGateUp>
+template <int BM, int BN, int GM, bool kGateUp, bool kPacked>
 struct StepCursor {
   int logical, mt, nt, kt;
   bool live;
-  TileSrc<BM, BN, kGateUp> src;
+  TileSrc<BM, BN, kGateUp, kPacked> src;
   __device__ void start(const TileWalk<GM>& walk, int logical_, int mt_, int nt_, const int32_t* tiles,
                         const bf16_t* A, const void* const* W0, const void* const* W1, int K) {
     logical = logical_, mt = mt_, nt = nt_, kt = 0, live = true;
@@ -350,7 +391,7 @@ struct StepCursor {
   }
 };
 
-template <bool kGateUp>
+template <bool kGateUp, bool kPacked>
 __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
@@ -378,7 +419,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     // ---------------- DMA waves ----------------
     const int dw = wave - Cfg::MW;
     const uint32_t k2 = (uint32_t)K * 2u;
-    StepCursor<Cfg::BM, Cfg::BN, Cfg::GM, kGateUp> ca, cb;  // next A step, next B step
+    StepCursor<Cfg::BM, Cfg::BN, Cfg::GM, kGateUp, kPacked> ca, cb;  // next A step, next B step
     ca.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
     cb.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
     auto issue_a = [&](int buf) {
@@ -397,7 +438,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
 #pragma unroll
       for (int i = 0; i < Cfg::OPS; ++i) {
         const int q = dw * Cfg::OPS + i;
-        cb.src.dma_b(dl, q, k2, base + q * 1024);
+        cb.src.dma_b(dl, lane, cb.kt, q, k2, base + q * 1024);
       }
       cb.advance(walk, tiles, A, W0, W1, K, KT);
     };
@@ -554,7 +595,7 @@ struct TileCfg {
   static_assert(DMA_PER_WAVE * (STAGES - 1) <= 63, "vmcnt range");
 };
 
-template <typename Cfg, bool kGateUp>
+template <typename Cfg, bool kGateUp, bool kPacked>
 __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
@@ -577,7 +618,8 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   const int wn = wave % Cfg::WGN;
   const uint32_t k2 = (uint32_t)K * 2u;
 
-  TileSrc<Cfg::BM, Cfg::BN, kGateUp> src;
+  static_assert(!kPacked || Cfg::BN == 256, "packed weights come in 256-row tiles");
+  TileSrc<Cfg::BM, Cfg::BN, kGateUp, kPacked> src;
   auto issue_stage = [&](int kstep, int buf) {
     char* sa = smem + buf * Cfg::STAGE_BYTES;
     char* sb = sa + Cfg::A_BYTES;
@@ -590,7 +632,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
       const int q = wave * Cfg::B_PER_WAVE + i;
-      src.dma_b(dl, q, k2, sb + q * 1024);
+      src.dma_b(dl, lane, kstep, q, k2, sb + q * 1024);
     }
   };
 
@@ -732,7 +774,7 @@ int persistent_grid(int64_t capacity, int64_t n_tiles_n, int64_t* grid) {
   return ASTRAI_MOE_OK;
 }
 
-template <bool kGateUp>
+template <bool kGateUp, bool kPacked>
 int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
                   const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s) {
   if (capacity == 0) return ASTRAI_MOE_OK;
@@ -740,23 +782,39 @@ int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const v
   const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
+  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
                      static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
                      (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C));
   return check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>");
 }
 
-template <typename Cfg, bool kGateUp>
+template <typename Cfg, bool kGateUp, bool kPacked>
 int launch(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
            const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  hipLaunchKernelGGL((gemm_mfma_kernel<Cfg, kGateUp>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
+  hipLaunchKernelGGL((gemm_mfma_kernel<Cfg, kGateUp, kPacked>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
                      static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
                      (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C));
   return check_launch(kGateUp ? "gemm_mfma_kernel<gate_up>" : "gemm_mfma_kernel<down>");
+}
+
+template <bool kPacked>
+int gate_up_dispatch(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
+                     const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, void* h, hipStream_t s) {
+  if (block_m == kMfmaBigBM)
+    return launch_stream<true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
+  return launch<SmallCfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
+}
+
+template <bool kPacked>
+int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
+                  const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, void* y, hipStream_t s) {
+  if (block_m == kMfmaBigBM)
+    return launch_stream<false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
+  return launch<SmallCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
 }
 
 }  // namespace
@@ -773,17 +831,32 @@ bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m, const void* 
 }
 
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
-                        const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, void* h, hipStream_t s) {
-  if (block_m == kMfmaBigBM)
-    return launch_stream<true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
-  return launch<SmallCfg, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
+                        const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, bool packed, void* h,
+                        hipStream_t s) {
+  return packed ? gate_up_dispatch<true>(x_perm, tiles, capacity, w_gate, w_gate, dim, dim_ffn, block_m, h, s)
+                : gate_up_dispatch<false>(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, block_m, h, s);
 }
 
 int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
-                     const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, void* y, hipStream_t s) {
-  if (block_m == kMfmaBigBM)
-    return launch_stream<false>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
-  return launch<SmallCfg, false>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
+                     const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, bool packed, void* y,
+                     hipStream_t s) {
+  return packed ? down_dispatch<true>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s)
+                : down_dispatch<false>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s);
+}
+
+int launch_pack(const void* w0, const void* w1, int64_t rows, int64_t k, bool gate_up, void* out, hipStream_t s) {
+  // rows: output rows of the projection (dim_ffn for gate/up, each; dim for down)
+  const int64_t n_tiles = gate_up ? rows / 128 : rows / 256;
+  const int64_t units = n_tiles * (k / kBK) * 256 * 8;
+  if (units == 0) return ASTRAI_MOE_OK;
+  const int64_t grid = std::min<int64_t>(ceil_div(units, 256), 65536);
+  if (gate_up)
+    hipLaunchKernelGGL((pack_kernel<true>), dim3((unsigned)grid), dim3(256), 0, s, static_cast<const bf16_t*>(w0),
+                       static_cast<const bf16_t*>(w1), n_tiles, (int)k, static_cast<uint4*>(out));
+  else
+    hipLaunchKernelGGL((pack_kernel<false>), dim3((unsigned)grid), dim3(256), 0, s, static_cast<const bf16_t*>(w0),
+                       static_cast<const bf16_t*>(w0), n_tiles, (int)k, static_cast<uint4*>(out));
+  return check_launch(gate_up ? "pack_kernel<gate_up>" : "pack_kernel<down>");
 }
 
 }  // namespace astrai_moe

@@ -180,13 +180,24 @@ def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: in
 
 
 def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
-                     n_experts: int, dim_ffn: int, block_m: int) -> torch.Tensor:
-    """h = up(x) * silu(gate(x)) over every expert's rows (mlp.py:22-23)."""
+                     n_experts: int, dim_ffn: int, block_m: int, packed: bool = False) -> torch.Tensor:
+    """h = up(x) * silu(gate(x)) over every expert's rows (mlp.py:22-23).
+
+    ``packed``: ``w_gate`` is a table of packed gate/up copies
+    (``moe_pack_gate_up``) and ``w_up`` is ignored; same results."""
     fn = _kernel("moe_gemm_gate_up")
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
+    if packed:
+        _check(
+            loader.library().astrai_moe_gemm_gate_up_packed(
+                x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(), code, n_rows, n_experts, dim,
+                dim_ffn, block_m, h.data_ptr(), _stream(x_perm)),
+            "moe_gemm_gate_up_packed",
+        )
+        return h
     _check(
         fn(x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(), w_up.data_ptr(), code, n_rows,
            n_experts, dim, dim_ffn, block_m, h.data_ptr(), _stream(x_perm)),
@@ -205,8 +216,11 @@ def _out_buffer(out: torch.Tensor | None, rows: int, cols: int, like: torch.Tens
 
 
 def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
-                  n_experts: int, dim: int, block_m: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """y = down(h) * routing weight over every expert's rows (mlp.py:24, :97)."""
+                  n_experts: int, dim: int, block_m: int, out: torch.Tensor | None = None,
+                  packed: bool = False) -> torch.Tensor:
+    """y = down(h) * routing weight over every expert's rows (mlp.py:24, :97).
+
+    ``packed``: ``w_down`` is a table of packed copies (``moe_pack_down``)."""
     fn = _kernel("moe_gemm_down")
     _require_gpu(h, "h", 2)
     code = _dtype_code(h, "h")
@@ -214,12 +228,53 @@ def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, so
     if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
         raise ValueError("sorted_w must hold one weight of h's dtype per row")
     y = _out_buffer(out, n_rows, dim, h)
+    if packed:
+        _check(
+            loader.library().astrai_moe_gemm_down_packed(
+                h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), sorted_w.data_ptr(), code, n_rows,
+                n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
+            "moe_gemm_down_packed",
+        )
+        return y
     _check(
         fn(h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), sorted_w.data_ptr(), code, n_rows,
            n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
         "moe_gemm_down",
     )
     return y
+
+
+def packed_supported(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
+    """Whether the packed-weight GEMMs take this expert shape (bf16, dim a
+    multiple of 256, dim_ffn a multiple of 128)."""
+    return (dtype == torch.bfloat16 and dim % 256 == 0 and dim_ffn % 128 == 0 and 0 < dim <= 1 << 22
+            and 0 < dim_ffn <= 1 << 22)
+
+
+def moe_pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """One expert's gate and up weights ([dim_ffn, dim] each) as one packed
+    copy for the packed GEMMs: ``[2 * dim_ffn, dim]`` bf16 in staged order."""
+    _require_gpu(w_gate, "w_gate", 2)
+    _require_gpu(w_up, "w_up", 2)
+    if w_gate.shape != w_up.shape or w_gate.dtype != w_up.dtype or w_gate.device != w_up.device:
+        raise ValueError("w_gate and w_up must match in shape, dtype and device")
+    code = _dtype_code(w_gate, "w_gate")
+    dim_ffn, dim = w_gate.shape
+    out = torch.empty(2 * dim_ffn, dim, dtype=w_gate.dtype, device=w_gate.device)
+    _check(loader.library().astrai_moe_pack_gate_up(w_gate.data_ptr(), w_up.data_ptr(), code, dim_ffn, dim,
+                                                    out.data_ptr(), _stream(w_gate)), "moe_pack_gate_up")
+    return out
+
+
+def moe_pack_down(w_down: torch.Tensor) -> torch.Tensor:
+    """One expert's down weight ([dim, dim_ffn]) as a packed copy (same size)."""
+    _require_gpu(w_down, "w_down", 2)
+    code = _dtype_code(w_down, "w_down")
+    dim, dim_ffn = w_down.shape
+    out = torch.empty(dim, dim_ffn, dtype=w_down.dtype, device=w_down.device)
+    _check(loader.library().astrai_moe_pack_down(w_down.data_ptr(), code, dim, dim_ffn, out.data_ptr(),
+                                                 _stream(w_down)), "moe_pack_down")
+    return out
 
 
 def moe_combine(y: torch.Tensor, token_pos: torch.Tensor, shared: torch.Tensor | None = None) -> torch.Tensor:
@@ -281,9 +336,10 @@ def moe_dense_mlp(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_d
 
 def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
                        w_down: torch.Tensor, dim_ffn: int, top_k: int,
-                       shared: torch.Tensor | None = None) -> torch.Tensor:
+                       shared: torch.Tensor | None = None, packed: bool = False) -> torch.Tensor:
     """Routed experts plus combine (mlp.py:84-100 and :71) for ``x [T, D]``
-    given the router logits and the experts' weight-pointer tables."""
+    given the router logits and the experts' weight-pointer tables (of packed
+    copies with ``packed``; ``w_up`` is then ignored)."""
     n_tokens, dim = x.shape
     n_experts = logits.shape[1]
     if n_tokens == 0:
@@ -291,6 +347,6 @@ def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tens
     block_m = select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
     route = moe_route(logits, top_k)
     perm = moe_permute(route, x, n_experts, block_m)
-    h = moe_gemm_gate_up(perm.x_perm, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m)
-    y = moe_gemm_down(h, perm.tiles, w_down, perm.sorted_w, n_experts, dim, block_m)
+    h = moe_gemm_gate_up(perm.x_perm, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m, packed=packed)
+    y = moe_gemm_down(h, perm.tiles, w_down, perm.sorted_w, n_experts, dim, block_m, packed=packed)
     return moe_combine(y, perm.token_pos, shared)

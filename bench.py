@@ -55,6 +55,8 @@ def _parse():
                    help="also time forward + backward (reported as train_*; value stays the forward)")
     p.add_argument("--graph", action="store_true",
                    help="also time the step as a replayed HIP graph (reported as graph_*; value stays eager)")
+    p.add_argument("--pack", action="store_true",
+                   help="read the layer's packed inference copy of the expert weights (opt-in)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="before timing, copy a buffer of this many MiB once (a plain copy kernel of known size "
                         "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -153,6 +155,7 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     layer, x = make_layer(w, dev)
+    layer.pack_weights = args.pack
     T = w.n_tokens
     if args.copy_probe_mib:
         src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
@@ -269,7 +272,8 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16" if bf16 else "f32",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) expert weights, random-init)",
-        "config": {**w.describe(), "parallelism": "single GPU, all experts resident"},
+        "config": {**w.describe(), "parallelism": "single GPU, all experts resident",
+                   "packed_weights": layer.uses_packed_weights(w.dtype)},
         "gemm_tflops": gemm_tflops,
         "gemm_frac_of_peak": gemm_tflops / peak,
         "roofline": roofline,

@@ -68,3 +68,11 @@ def test_graph_shapes(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, n_tok):
     layer = _layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype)
     x = torch.randn(1, n_tok, dim, device=gpu).to(dtype)
     _check_graph(layer, x)
+
+
+def test_graph_packed_weights(gpu):
+    # the packed copy is built by the warm-up call, outside the capture
+    layer = _layer(gpu, 512, 256, 16, 1, 4, torch.bfloat16)
+    layer.pack_weights = True
+    x = torch.randn(1, 200, 512, device=gpu).to(torch.bfloat16)
+    _check_graph(layer, x)

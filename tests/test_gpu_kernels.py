@@ -175,6 +175,59 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
         torch.testing.assert_close(y[a:b], y_ref, **tol)
 
 
+def _packed_layout(w0, w1, tile_rows):
+    """Expected packed order of one expert's weight: per column tile of 256
+    rows (gate/up: ``tile_rows`` = 128 gate rows then the same 128 up rows;
+    down: 256 rows of ``w0``) and per 64-wide K step, a block of 256 rows x 8
+    chunks of 8 elements in which row r keeps its chunk c at position
+    c ^ ((r >> 1) & 7)."""
+    n, k = w0.shape
+    if w1 is not None:
+        w = torch.cat([w0.view(n // tile_rows, tile_rows, k), w1.view(n // tile_rows, tile_rows, k)], 1)
+    else:
+        w = w0.view(n // tile_rows, tile_rows, k)
+    nt = w.shape[0]
+    blocks = w.view(nt, 256, k // 64, 8, 8).permute(0, 2, 1, 3, 4)  # [tile, kstep, row, chunk, 8]
+    r = torch.arange(256, device=w0.device)[:, None]
+    src_chunk = torch.arange(8, device=w0.device)[None, :] ^ ((r >> 1) & 7)
+    idx = src_chunk[None, None, :, :, None].expand(nt, k // 64, 256, 8, 8)
+    return blocks.gather(3, idx).reshape(-1, k)
+
+
+@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
+    (2048, 8, 2, 1024, 1536),  # 256-row tiles
+    (300, 16, 4, 512, 256),  # 32-row tiles
+    (64, 128, 8, 4096, 1536),  # decode-sized loads over many experts
+    (16384, 4, 2, 256, 128),  # one column tile per expert for gate/up
+])
+def test_packed_gemms_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
+    dtype = torch.bfloat16
+    assert ops.packed_supported(dim, dim_ffn, dtype)
+    route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=7)
+    g = torch.Generator(device=gpu).manual_seed(8)
+    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=9)
+    bm = ops.select_block_m(n_tok, n_exp, top_k, dim, dim_ffn, dtype)
+    perm = ops.moe_permute(route, x, n_exp, bm)
+    tg = ops.expert_weight_table([e.gate for e in experts], (dim_ffn, dim))
+    tu = ops.expert_weight_table([e.up for e in experts], (dim_ffn, dim))
+    td = ops.expert_weight_table([e.down for e in experts], (dim, dim_ffn))
+    h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm)
+    pg = [ops.moe_pack_gate_up(e.gate, e.up) for e in experts]
+    pd = [ops.moe_pack_down(e.down) for e in experts]
+    for e in (0, n_exp - 1):
+        assert torch.equal(pg[e], _packed_layout(experts[e].gate, experts[e].up, 128))
+        assert torch.equal(pd[e], _packed_layout(experts[e].down, None, 256))
+    tpg = ops.expert_weight_table(pg, (2 * dim_ffn, dim))
+    tpd = ops.expert_weight_table(pd, (dim, dim_ffn))
+    hp = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tpg, tpg, n_exp, dim_ffn, bm, packed=True)
+    yp = ops.moe_gemm_down(h, perm.tiles, tpd, perm.sorted_w, n_exp, dim, bm, packed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(hp, h)
+    assert torch.equal(yp, y)
+
+
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,n_shared,dtype", [
     (1000, 8, 2, 256, 0, torch.bfloat16),
     (513, 16, 5, 128, 0, torch.bfloat16),

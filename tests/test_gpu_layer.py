@@ -134,3 +134,46 @@ def test_checkpoint_load_into_live_layer(gpu, tmp_path):
         assert not torch.equal(a(x), out_b)
         check_layer(a, x, "swapped gate weights")
 
+
+
+def test_packed_weights_match_live_weights_and_follow_updates(gpu, tmp_path):
+    # bf16 shapes the matrix-core kernels take are read from the layer's packed
+    # copy in inference; its results must equal the live-weight path bit for
+    # bit, and in-place updates, checkpoint loads and swapped parameters must
+    # reach it
+    from safetensors.torch import load_file, save_file
+
+    a = _random_layer(gpu, 512, 256, 16, 1, 4, torch.bfloat16, seed=0)
+    b = _random_layer(gpu, 512, 256, 16, 1, 4, torch.bfloat16, seed=1)
+    a.pack_weights = True
+    assert a.uses_packed_weights(torch.bfloat16)
+    x = torch.randn(3, 101, 512, device=gpu).to(torch.bfloat16)
+
+    def both(layer):
+        layer.pack_weights = True
+        p = layer(x)
+        layer.pack_weights = False
+        q = layer(x)
+        layer.pack_weights = True
+        torch.cuda.synchronize()
+        assert torch.equal(p, q)
+        return p
+
+    with torch.no_grad():
+        out0 = both(a)
+        check_layer(a, x, "packed")
+        a.routed_experts[3].gate.weight.mul_(1.5)  # in place: version counter moves
+        a.routed_experts[9].down.weight.neg_()
+        out1 = both(a)
+        assert not torch.equal(out0, out1)
+        check_layer(a, x, "packed after in-place update")
+        path = tmp_path / "b.safetensors"
+        save_file({k: v.cpu() for k, v in b.state_dict().items()}, str(path))
+        a.load_state_dict(load_file(str(path), device=str(gpu)))
+        assert torch.equal(both(a), b(x))
+        c = _random_layer(gpu, 512, 256, 16, 1, 4, torch.bfloat16, seed=2)
+        for m_a, m_c in zip(a.routed_experts, c.routed_experts):
+            m_a.up.weight = m_c.up.weight
+        out3 = both(a)
+        assert not torch.equal(out3, b(x))
+        check_layer(a, x, "packed after swapped up weights")

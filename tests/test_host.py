@@ -175,6 +175,16 @@ def test_abi_rejects_bad_arguments_with_message():
     assert rc == -1 and "tile list" in loader.last_error()
     rc = lib.astrai_moe_combine(1, 1, None, 2, 1, 4, 2, 8, 1, None)
     assert rc == -1 and "n_shared" in loader.last_error()
+    rc = lib.astrai_moe_pack_gate_up(None, None, 0, 128, 64, None, None)
+    assert rc == -1 and "bf16 only" in loader.last_error()
+    rc = lib.astrai_moe_pack_gate_up(None, None, 1, 100, 64, None, None)
+    assert rc == -1 and "dim_ffn % 128" in loader.last_error()
+    rc = lib.astrai_moe_pack_gate_up(None, None, 1, 128, 64, None, None)
+    assert rc == -1 and "null buffer" in loader.last_error()
+    rc = lib.astrai_moe_pack_down(None, 1, 200, 64, None, None)
+    assert rc == -1 and "dim % 256" in loader.last_error()
+    rc = lib.astrai_moe_pack_down(8, 1, 256, 64, 32, None)
+    assert rc == -1 and "16-byte aligned" in loader.last_error()
     # Empty inputs are a valid no-op.
     assert lib.astrai_moe_route(None, 1, 0, 8, 2, None, None, None, None) == 0
     assert lib.astrai_moe_combine(None, None, None, 0, 1, 0, 2, 8, None, None) == 0
@@ -204,6 +214,19 @@ def test_block_m_policy():
     assert ops.select_block_m(64, 128, 8, 4096, 1536, bf) == 32
     assert ops.select_block_m(1024, 8, 2, 512, 1024, torch.float32) == 64
     assert ops.select_block_m(100, 4, 2, 8, 16, bf) == 64  # shapes the MFMA kernels do not tile
+
+
+def test_packed_weights_follow_the_matrix_core_policy():
+    # the layer packs exactly the shapes the matrix-core kernels take
+    for dim, dim_ffn in [(4096, 14336), (2048, 1408), (256, 512), (512, 256), (96, 80), (8, 16), (256, 64)]:
+        for dtype in (torch.bfloat16, torch.float32):
+            bm = ops.select_block_m(1024, 8, 2, dim, dim_ffn, dtype)
+            assert ops.packed_supported(dim, dim_ffn, dtype) == (bm in (32, 256)), (dim, dim_ffn, dtype)
+    m = DeepSeekMoE(512, 256, 4, n_shared_experts=0)
+    assert not m.pack_weights and not m.uses_packed_weights(torch.bfloat16)  # opt-in
+    m.pack_weights = True
+    assert m.uses_packed_weights(torch.bfloat16) and not m.uses_packed_weights(torch.float32)
+    assert not DeepSeekMoE(8, 16, 4, n_shared_experts=0).uses_packed_weights(torch.bfloat16)
 
 
 def test_ops_validate_before_launch():
