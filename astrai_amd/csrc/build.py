@@ -59,7 +59,8 @@ def register(name: str, sources: list[str] | None = None, **kwargs) -> None:
 
 register("moe_route")
 register("moe_permute")
-register("moe_gemm", sources=[str(KERNELS_DIR / "moe_gemm.hip"), str(KERNELS_DIR / "moe_gemm_mfma.hip")])
+register("moe_gemm", sources=[str(KERNELS_DIR / "moe_gemm.hip"), str(KERNELS_DIR / "moe_gemm_mfma.hip"),
+                              str(KERNELS_DIR / "moe_gemm_bwd.hip")])
 register("moe_combine")
 register("capi")
 

@@ -1,0 +1,140 @@
+// Device helpers shared by the CDNA4 matrix-core GEMMs (gfx950): operand
+// vector types, LDS DMA and its waits, the persistent XCD-aware tile walk
+// and the per-lane DMA chunk choice of the 16-byte LDS swizzle.
+#pragma once
+
+#include "moe_gemm.h"
+
+#include <algorithm>
+#include <atomic>
+#include <utility>
+
+namespace astrai_moe {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kBK = 64;             // K elements per stage
+constexpr int kRowBytes = kBK * 2;  // 128 bytes per staged row
+constexpr int kXcds = 8;
+
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__device__ inline void lds_dma_16(const void* gsrc, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
+                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until at most min(pending, MAXP) groups of PER DMA ops are in flight.
+template <int PER, int MAXP>
+__device__ inline void wait_groups(int pending) {
+  if constexpr (MAXP <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (pending >= MAXP)
+      wait_vmcnt<MAXP * PER>();
+    else
+      wait_groups<PER, MAXP - 1>(pending);
+  }
+}
+
+__device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }  // lgkmcnt(0)
+
+// Barriers are s_barrier after explicit waits: LDS-DMA completion is tracked
+// by vmcnt, so the waits are placed by hand rather than by a fence.
+__device__ inline void lds_barrier() {
+  wait_lds();
+  __builtin_amdgcn_s_barrier();
+}
+
+// The persistent tile walk. Round r takes logical tile r * G + slot, where
+// slot gives the workgroups of one XCD a contiguous range of logical tiles;
+// logical tiles walk GM row tiles for every column tile. Dead row tiles (past
+// the live count the tile list reports) are skipped.
+template <int GM>
+struct TileWalk {
+  int G, total, n_live, group_size, capacity;
+  __device__ TileWalk(const int32_t* tiles, int capacity_, int n_tiles_n)
+      : G((int)gridDim.x), total(capacity_ * n_tiles_n), n_live(min(tiles[0], tiles[2])),
+        group_size(GM * n_tiles_n), capacity(capacity_) {}
+  __device__ int first_slot() const {
+    const int bid = blockIdx.x;
+    return (G % kXcds == 0) ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
+  }
+  __device__ bool decode(int logical, int& mt, int& nt) const {
+    const int first_m = (logical / group_size) * GM;
+    const int gm = min(GM, capacity - first_m);
+    const int in_group = logical - (first_m / GM) * group_size;
+    mt = first_m + in_group % gm;
+    nt = in_group / gm;
+    return mt < n_live;
+  }
+  // the first live logical tile at or after `logical` in this workgroup's sequence (>= total: none)
+  __device__ int seek(int logical, int& mt, int& nt) const {
+    while (logical < total && !decode(logical, mt, nt)) logical += G;
+    return logical;
+  }
+};
+
+// One 8-row DMA group of a stage: lane l loads row (l >> 3) of the group and
+// physical chunk l & 7, which holds logical chunk (l & 7) ^ ((row >> 1) & 7).
+// The source offsets are 32-bit byte offsets from uniform bases.
+struct DmaLane {
+  uint32_t chk0, chk1;  // byte offsets of the lane's chunk in even / odd 8-row groups
+  int row;              // row within the 8-row group
+  __device__ DmaLane(int lane, int kstep) {
+    row = lane >> 3;
+    const uint32_t koff = (uint32_t)kstep * kRowBytes;
+    chk0 = (uint32_t)(((lane & 7) ^ ((row >> 1) & 7)) << 4) + koff;
+    chk1 = (uint32_t)(((lane & 7) ^ (((row >> 1) + 4) & 7)) << 4) + koff;
+  }
+  // (arithmetic select: q's parity may be a runtime value)
+  __device__ uint32_t chunk(int q) const {
+    const uint32_t m = 0u - (uint32_t)(q & 1);
+    return (chk0 & ~m) | (chk1 & m);
+  }
+};
+
+// ---- host side of the persistent launches ----
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// Compute units of the current device (one persistent workgroup each).
+int cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Grid of a persistent launch: one workgroup per compute unit (the LDS
+// footprint allows no more), each walking its share of the tile list.
+int persistent_grid(int64_t capacity, int64_t n_tiles_n, int64_t* grid) {
+  const int64_t total = capacity * n_tiles_n;
+  if (total >= (1ll << 31))
+    return fail(ASTRAI_MOE_EINVAL, "gemm: %lld tiles exceed the tile-index range", (long long)total);
+  *grid = std::min<int64_t>(total, cu_count());
+  return ASTRAI_MOE_OK;
+}
+
+}  // namespace
+}  // namespace astrai_moe

@@ -31,6 +31,40 @@ int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
                      int64_t dim_ffn, int64_t dim, int block_m, bool packed,
                      void* y, hipStream_t s);
 
+// Training forward (256-row tiles): as launch_mfma_gate_up / launch_mfma_down,
+// also storing the bf16 gate and up projections (g, u: [rows, dim_ffn]) or
+// the unweighted bf16 expert output (y_unweighted: [rows, dim]).
+int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles,
+                             int64_t capacity, const void* const* w_gate,
+                             const void* const* w_up, int64_t dim,
+                             int64_t dim_ffn, void* h, void* g, void* u,
+                             hipStream_t s);
+int launch_mfma_down_save(const void* h, const int32_t* tiles,
+                          int64_t capacity, const void* const* w_down,
+                          const void* sorted_w, int64_t dim_ffn, int64_t dim,
+                          void* y, void* y_unweighted, hipStream_t s);
+
+// Backward (moe_gemm_bwd.hip), bf16, 256-row tile lists:
+// dy = dout[sorted_token] * sorted_w and dw_rows = sum(dout[tok] * y) per row;
+int launch_row_grad(const void* dout, const int32_t* sorted_token,
+                    const void* sorted_w, const void* y, int64_t n_rows,
+                    int64_t dim, void* dy, void* dw_rows, hipStream_t s);
+// dg, du [rows, dim_ffn] from dy [rows, dim], W_down [dim, dim_ffn] and the
+// saved g, u;
+int launch_dgrad_down(const void* dy, const int32_t* tiles, int64_t capacity,
+                      const void* const* w_down, const void* g, const void* u,
+                      int64_t dim, int64_t dim_ffn, void* dg, void* du,
+                      hipStream_t s);
+// dx [rows, n] = bf16(d . W[e]) (+ add, rounded again), W[e] [k, n];
+int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity,
+                    const void* const* w, int64_t k, int64_t n,
+                    const void* add, void* dx, hipStream_t s);
+// dw[e] [m, n] = a[rows_e]^T . b[rows_e] for every expert with rows
+// (a: [rows, m], b: [rows, n]); experts without rows are not written.
+int launch_wgrad(const void* a, const void* b, const int32_t* offsets,
+                 int n_experts, int64_t m, int64_t n, void* dw,
+                 hipStream_t s);
+
 // Packs one expert's weight for the packed GEMMs: gate/up (w0 = gate, w1 =
 // up, each [rows, k]) or down (w0 = [rows, k]).
 int launch_pack(const void* w0, const void* w1, int64_t rows, int64_t k,

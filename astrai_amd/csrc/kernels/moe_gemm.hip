@@ -276,3 +276,121 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
   return launch_mfma_down(h, tiles, capacity, w_packed, sorted_w, dim_ffn, dim, block_m, true, y,
                           static_cast<hipStream_t>(stream));
 }
+
+// ---------------------------------------------------------------------------
+// Training forward and backward (bf16, matrix-core shapes, 256-row tiles).
+// ---------------------------------------------------------------------------
+
+static int check_train(const char* who, int dtype, int64_t dim, int64_t dim_ffn, int block_m) {
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "%s: the backward kernels are bf16 only (dtype %d)", who, dtype);
+  ASTRAI_REQUIRE(block_m == kMfmaBigBM, "%s: needs the 256-row tile list (block_m %d)", who, block_m);
+  ASTRAI_REQUIRE(dim > 0 && dim_ffn > 0 && dim % 256 == 0 && dim_ffn % 128 == 0 && dim <= (1ll << 22) &&
+                     dim_ffn <= (1ll << 22),
+                 "%s: needs dim %% 256 == 0 and dim_ffn %% 128 == 0 (got %lld, %lld)", who, (long long)dim,
+                 (long long)dim_ffn);
+  return ASTRAI_MOE_OK;
+}
+
+extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles, int64_t tiles_len,
+                                             const void* const* w_gate, const void* const* w_up, int dtype,
+                                             int64_t n_rows, int n_experts, int64_t dim, int64_t dim_ffn,
+                                             int block_m, void* h, void* g, void* u, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_gate_up_train", x_perm, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn,
+                        block_m, h);
+  if (rc) return rc;
+  if ((rc = check_train("gemm_gate_up_train", dtype, dim, dim_ffn, block_m))) return rc;
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_gate && w_up && g && u, "gemm_gate_up_train: null weight table or output");
+  ASTRAI_REQUIRE(aligned16_ptr(x_perm) && aligned16_ptr(h) && aligned16_ptr(g) && aligned16_ptr(u),
+                 "gemm_gate_up_train: buffers must be 16-byte aligned");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, g, u,
+                                  static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, int64_t tiles_len,
+                                          const void* const* w_down, const void* sorted_w, int dtype,
+                                          int64_t n_rows, int n_experts, int64_t dim_ffn, int64_t dim, int block_m,
+                                          void* y, void* y_unweighted, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_down_train", h, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m, y);
+  if (rc) return rc;
+  if ((rc = check_train("gemm_down_train", dtype, dim, dim_ffn, block_m))) return rc;
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_down && sorted_w && y_unweighted, "gemm_down_train: null weight table, row weights or output");
+  ASTRAI_REQUIRE(aligned16_ptr(h) && aligned16_ptr(y) && aligned16_ptr(y_unweighted),
+                 "gemm_down_train: buffers must be 16-byte aligned");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  return launch_mfma_down_save(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, y, y_unweighted,
+                               static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token, const void* sorted_w,
+                                   const void* y_unweighted, int dtype, int64_t n_rows, int64_t dim, void* dy,
+                                   void* dw_rows, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "row_grad: bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(n_rows >= 0 && n_rows < (1ll << 31), "row_grad: n_rows must be in [0, 2^31)");
+  ASTRAI_REQUIRE(dim > 0 && dim % 8 == 0, "row_grad: needs dim %% 8 == 0 (got %lld)", (long long)dim);
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(dout && sorted_token && sorted_w && y_unweighted && dy && dw_rows, "row_grad: null buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(dout) && aligned16_ptr(y_unweighted) && aligned16_ptr(dy),
+                 "row_grad: buffers must be 16-byte aligned");
+  return launch_row_grad(dout, sorted_token, sorted_w, y_unweighted, n_rows, dim, dy, dw_rows,
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles, int64_t tiles_len,
+                                          const void* const* w_down, const void* g, const void* u, int dtype,
+                                          int64_t n_rows, int n_experts, int64_t dim, int64_t dim_ffn, int block_m,
+                                          void* dg, void* du, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_dgrad_down", dy, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn, block_m,
+                        dg);
+  if (rc) return rc;
+  if ((rc = check_train("gemm_dgrad_down", dtype, dim, dim_ffn, block_m))) return rc;
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(w_down && g && u && du, "gemm_dgrad_down: null weight table or buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(dy) && aligned16_ptr(g) && aligned16_ptr(u) && aligned16_ptr(dg) &&
+                     aligned16_ptr(du),
+                 "gemm_dgrad_down: buffers must be 16-byte aligned");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  return launch_dgrad_down(dy, tiles, capacity, w_down, g, u, dim, dim_ffn, dg, du, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, const int32_t* tiles, int64_t tiles_len,
+                                             const void* const* w_gate, const void* const* w_up, int dtype,
+                                             int64_t n_rows, int n_experts, int64_t dim_ffn, int64_t dim,
+                                             int block_m, void* dx_perm, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_dgrad_gate_up", dg, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m,
+                        dx_perm);
+  if (rc) return rc;
+  if ((rc = check_train("gemm_dgrad_gate_up", dtype, dim, dim_ffn, block_m))) return rc;
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(du && w_gate && w_up, "gemm_dgrad_gate_up: null weight table or buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(dg) && aligned16_ptr(du) && aligned16_ptr(dx_perm),
+                 "gemm_dgrad_gate_up: buffers must be 16-byte aligned");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // dx_perm = bf16(dg . W_gate), then dx_perm = bf16(bf16(du . W_up) + dx_perm)
+  if ((rc = launch_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
+  return launch_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
+}
+
+extern "C" int astrai_moe_gemm_wgrad(const void* a, const void* b, const int32_t* expert_offsets, int dtype,
+                                     int64_t n_rows, int n_experts, int64_t m, int64_t n, void* dw, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_wgrad: bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(n_rows >= 0 && n_rows < (1ll << 31), "gemm_wgrad: n_rows must be in [0, 2^31)");
+  ASTRAI_REQUIRE(n_experts >= 1 && n_experts <= ASTRAI_MOE_MAX_EXPERTS, "gemm_wgrad: n_experts must be in [1, %d]",
+                 ASTRAI_MOE_MAX_EXPERTS);
+  ASTRAI_REQUIRE(m > 0 && n > 0 && m % 8 == 0 && n % 8 == 0 && m <= (1ll << 22) && n <= (1ll << 22),
+                 "gemm_wgrad: needs m %% 8 == 0 and n %% 8 == 0 (got %lld, %lld)", (long long)m, (long long)n);
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(a && b && expert_offsets && dw, "gemm_wgrad: null buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(a) && aligned16_ptr(b) && aligned16_ptr(dw),
+                 "gemm_wgrad: buffers must be 16-byte aligned");
+  return launch_wgrad(a, b, expert_offsets, n_experts, m, n, dw, static_cast<hipStream_t>(stream));
+}

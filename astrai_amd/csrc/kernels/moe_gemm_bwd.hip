@@ -1,0 +1,572 @@
+// Backward of the routed experts on CDNA4 matrix cores (gfx950): the grouped
+// input-gradient (dgrad) and weight-gradient (wgrad) GEMMs of the SwiGLU
+// experts, and the per-row gradient of the weighted combine.
+//
+// The reference layer is plain torch (astrai/model/components/mlp.py:22-25,
+// 89-98) and autograd differentiates it op by op; per expert e with rows R_e:
+//   dy   = dout[tok] * w                       (row_grad_kernel, also dw)
+//   dh   = dy . W_down                         [R_e, F]  dgrad, W_down [D, F]
+//   du   = dh * silu(g),  dg = silu'(g) * (dh * u)         (dgrad epilogue)
+//   dx   = bf16(dg . W_gate) + bf16(du . W_up) [R_e, D]  two dgrad launches,
+//          the second adding the first's result in its epilogue (autograd
+//          rounds each linear's input gradient, then their sum)
+//   dW_down = dy^T . h,  dW_gate = dg^T . x,  dW_up = du^T . x   (wgrad)
+// with g, u the bf16 gate / up projections and h = u * silu(g) saved by the
+// training forward.
+//
+// Operand layouts. The forward kernels read both operands K-contiguous. Here
+// the dgrad weight operand (W_down [K = D, N = F], W_gate/W_up [K = F, N = D])
+// and both wgrad operands ([K = rows, M or N]) are MN-contiguous: a stage
+// holds 64 K-rows of 256 columns (512 bytes each), copied as they lie by the
+// LDS DMA, and the fragments are read with ds_read_b64_tr_b16. That
+// instruction works on groups of 16 lanes: source lane 4 i + q reads 4
+// consecutive 16-bit values, and lane 4 q' + c of the group receives value c
+// of source lanes q', 4 + q', 8 + q', 12 + q'. When lane 4 i + q of group g
+// reads K-row 8 g + 4 h + i at columns 16 s + 4 q, lane j of group g receives
+// K = 8 g + 4 h + 0..3 of column 16 s + j: two such reads (h = 0, 1) give
+// exactly the per-lane layout of a v_mfma_f32_16x16x32_bf16 operand (index
+// l % 16, K 8 (l / 16) .. + 7).
+//
+// MN-major swizzle: the 32-byte segment s of K-row k is stored at segment
+// s ^ z(k) of its 256-byte half, z(k) = (k & 3) | ((k >> 3) & 1) << 2. The
+// 32 lanes of one half-wave read rows {0..3, 8..11} + const of one segment;
+// z maps them to 8 distinct 32-byte bank groups. Since z(k) depends only on
+// the lane here (bits 2 and 4+ of k come from the K half and the read), a
+// fragment's address is the lane's base xor (segment << 5).
+//
+// Schedule: the prefill kernel's (moe_gemm_mfma.hip): persistent, one
+// workgroup per CU, 256 x 256 output tiles, 8 matrix-core waves of 128 x 64
+// and 4 LDS-DMA waves, activations in 2 stages and the second operand in 3,
+// one barrier per 64-K step, the next step's first fragments prefetched
+// across tile boundaries. dgrad walks the forward's 256-row tile list; wgrad
+// walks (expert, M tile, N tile) with K = the expert's rows, rows past the
+// expert's end read from a zero row.
+#include "mfma_tile.h"
+
+#include <type_traits>
+
+namespace astrai_moe {
+namespace {
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x8_t __attribute__((ext_vector_type(8)));
+
+enum class Bwd { kDgradDown, kDgradIn, kWgrad };
+
+// Source of K-rows past an expert's last row in wgrad (zero contribution).
+__device__ __attribute__((aligned(512))) uint4 g_zero_row[32] = {};
+
+struct BwdArgs {
+  const bf16_t* a0;          // A: dy / dg / du (dgrad, K-major [rows, K]); wgrad: A [rows, M]
+  const void* const* w0;     // dgrad: weight table (W_down / W_gate / W_up, each [K, N])
+  const bf16_t* b_act;       // wgrad: B [rows, N]
+  const int32_t* tiles;      // dgrad: 256-row tile list
+  const int32_t* offsets;    // wgrad: expert row offsets [E + 1]
+  const bf16_t* e0;          // dgrad down epilogue: g [rows, N]; dgrad in: addend or null
+  const bf16_t* e1;          // dgrad down epilogue: u [rows, N]
+  bf16_t* c0;                // dgrad down: dg; dgrad in: dx; wgrad: dW [E, M, N]
+  bf16_t* c1;                // dgrad down: du
+  int K;                     // dgrad: K
+  int M, N;                  // wgrad: M x N per expert; dgrad: N
+  int n_tiles_m, n_tiles_n;  // column tiles (dgrad), M / N tiles (wgrad)
+  int capacity;              // dgrad: tile-list capacity
+  int n_experts;             // wgrad
+};
+
+struct BwdCfg {
+  static constexpr int BM = 256, BN = 256, GM = 8;
+  static constexpr int WGM = 2, WGN = 4, MW = 8, DW = 4;
+  static constexpr int WAVES = MW + DW, THREADS = WAVES * 64;
+  static constexpr int WM = BM / WGM, WN = BN / WGN;
+  static constexpr int A_BYTES = 32768, B_BYTES = 32768;
+  static constexpr int A_STAGES = 2, B_STAGES = 3;
+  static constexpr int A_OFF = 0, B_OFF = A_STAGES * A_BYTES;
+  static constexpr int LDS = B_OFF + B_STAGES * B_BYTES;  // 160 KB
+  static constexpr int OPS = A_BYTES / 1024 / DW;         // 8 DMA ops per DMA wave per operand and step
+  static constexpr int RG = 2, AR = 4, PD = 2;
+  static constexpr int MN_ROW = 512;                       // bytes of one MN-major K-row (256 columns)
+  static_assert(BM * 64 * 2 == A_BYTES && BN * 64 * 2 == B_BYTES, "64-K stages");
+  static_assert(LDS <= 160 * 1024, "LDS");
+  static_assert(3 * OPS <= 63, "vmcnt range");
+};
+
+struct TileInfo {
+  int e, mt, nt, row0, rows, ksteps;
+};
+
+// dgrad: the forward's tile walk over (row tile, column tile), K fixed.
+struct RowTileWalk {
+  TileWalk<BwdCfg::GM> w;
+  const int32_t* tiles;
+  int ksteps;
+  int G, total;
+  __device__ explicit RowTileWalk(const BwdArgs& p)
+      : w(p.tiles, p.capacity, p.n_tiles_n), tiles(p.tiles), ksteps(p.K / kBK), G(w.G), total(w.total) {}
+  __device__ int first_slot() const { return w.first_slot(); }
+  __device__ int seek(int logical, TileInfo& t) const {
+    logical = w.seek(logical, t.mt, t.nt);
+    if (logical < total) {
+      const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)t.mt * ASTRAI_MOE_TILE_STRIDE;
+      t.e = ti[0];
+      t.row0 = ti[1];
+      t.rows = min(BwdCfg::BM, ti[2] - t.row0);
+      t.ksteps = ksteps;
+    }
+    return logical;
+  }
+};
+
+// wgrad: (expert, M tile, N tile), GM M tiles walked per N tile; experts
+// without rows are skipped; K = the expert's rows in steps of 64.
+struct ExpertWalk {
+  const int32_t* off;
+  int MT, NT, per_e, G, total;
+  __device__ explicit ExpertWalk(const BwdArgs& p)
+      : off(p.offsets), MT(p.n_tiles_m), NT(p.n_tiles_n), per_e(p.n_tiles_m * p.n_tiles_n), G((int)gridDim.x),
+        total(p.n_experts * p.n_tiles_m * p.n_tiles_n) {}
+  __device__ int first_slot() const {
+    const int bid = blockIdx.x;
+    return (G % kXcds == 0) ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
+  }
+  __device__ bool decode(int logical, TileInfo& t) const {
+    t.e = logical / per_e;
+    const int r = logical - t.e * per_e;
+    const int first_m = (r / (BwdCfg::GM * NT)) * BwdCfg::GM;
+    const int gm = min(BwdCfg::GM, MT - first_m);
+    const int in_group = r - first_m * NT;
+    t.mt = first_m + in_group % gm;
+    t.nt = in_group / gm;
+    t.row0 = off[t.e];
+    t.rows = off[t.e + 1] - t.row0;
+    t.ksteps = (t.rows + kBK - 1) / kBK;
+    return t.rows > 0;
+  }
+  __device__ int seek(int logical, TileInfo& t) const {
+    while (logical < total && !decode(logical, t)) logical += G;
+    return logical;
+  }
+};
+
+__device__ __forceinline__ int mn_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+
+// Byte offset, within a 512-byte MN-major K-row, of what DMA lane `lane` of
+// op q stores: the op fills K-rows 2 q and 2 q + 1; slot p = lane & 31 holds
+// half (p & 1) of segment (p >> 1) ^ z(k).
+__device__ __forceinline__ uint32_t mn_src_col(int q, int lane) {
+  const int kr = 2 * q + (lane >> 5);
+  const int p = lane & 31;
+  return (uint32_t)((((p >> 1) ^ mn_swz(kr)) << 5) | ((p & 1) << 4));
+}
+
+// One DMA op of an MN-major stage: K-rows krow0 + 2 q + {0, 1} of `base`
+// (rows at or past `valid_rows` read the zero row), columns from byte col0,
+// clamped to the last 16 bytes before col_end (those columns are masked in
+// the epilogue).
+__device__ __forceinline__ void dma_mn(const char* base, int krow0, int valid_rows, uint32_t pitch, uint32_t col0,
+                                       uint32_t col_end, int lane, int q, char* lds) {
+  const int row = krow0 + 2 * q + (lane >> 5);
+  const uint32_t col = min(col0 + mn_src_col(q, lane), col_end - 16u);
+  const char* src = row < valid_rows ? base + (int64_t)row * pitch + col
+                                     : reinterpret_cast<const char*>(g_zero_row) + (col & 511u);
+  lds_dma_16(src, lds);
+}
+
+// Per-tile global bases of both operands.
+template <Bwd kMode>
+struct BwdSrc {
+  const char* a0 = nullptr;
+  const char* b0 = nullptr;
+  int rows = 0;
+  uint32_t a_col0 = 0, b_col0 = 0;
+  __device__ void setup(const BwdArgs& p, const TileInfo& t) {
+    rows = t.rows;
+    if constexpr (kMode == Bwd::kWgrad) {
+      a0 = reinterpret_cast<const char*>(p.a0 + (int64_t)t.row0 * p.M);
+      b0 = reinterpret_cast<const char*>(p.b_act + (int64_t)t.row0 * p.N);
+      a_col0 = (uint32_t)t.mt * BwdCfg::MN_ROW;
+      b_col0 = (uint32_t)t.nt * BwdCfg::MN_ROW;
+    } else {
+      a0 = reinterpret_cast<const char*>(p.a0 + (int64_t)t.row0 * p.K);
+      b0 = static_cast<const char*>(p.w0[t.e]);
+      b_col0 = (uint32_t)t.nt * BwdCfg::MN_ROW;
+    }
+  }
+  // 8-row group (dgrad, K-major) or 2-K-row group (wgrad, MN-major) q of
+  // step kstep's A stage.
+  __device__ void dma_a(const BwdArgs& p, int lane, int kstep, int q, char* lds) const {
+    if constexpr (kMode == Bwd::kWgrad) {
+      dma_mn(a0, kstep * kBK, rows, (uint32_t)p.M * 2u, a_col0, (uint32_t)p.M * 2u, lane, q, lds);
+    } else {
+      const DmaLane dl(lane, kstep);
+      const uint32_t row = (uint32_t)min(q * 8 + dl.row, rows - 1);
+      lds_dma_16(a0 + (row * ((uint32_t)p.K * 2u) + dl.chunk(q)), lds);
+    }
+  }
+  // 2-K-row group q of step kstep's B stage (MN-major in every mode).
+  __device__ void dma_b(const BwdArgs& p, int lane, int kstep, int q, char* lds) const {
+    if constexpr (kMode == Bwd::kWgrad) {
+      dma_mn(b0, kstep * kBK, rows, (uint32_t)p.N * 2u, b_col0, (uint32_t)p.N * 2u, lane, q, lds);
+    } else {
+      dma_mn(b0, kstep * kBK, 0x7fffffff, (uint32_t)p.N * 2u, b_col0, (uint32_t)p.N * 2u, lane, q, lds);
+    }
+  }
+};
+
+template <Bwd kMode, typename Walk>
+struct BwdCursor {
+  int logical, kt;
+  bool live;
+  TileInfo t;
+  BwdSrc<kMode> src;
+  __device__ void start(const BwdArgs& p, int logical_, const TileInfo& t_) {
+    logical = logical_, t = t_, kt = 0, live = true;
+    src.setup(p, t);
+  }
+  __device__ void advance(const BwdArgs& p, const Walk& walk) {
+    if (++kt == t.ksteps) {
+      kt = 0;
+      logical = walk.seek(logical + walk.G, t);
+      live = logical < walk.total;
+      if (live) src.setup(p, t);
+    }
+  }
+};
+
+__device__ __forceinline__ bf16x8_t lds_tr_pair(const char* smem, uint32_t addr) {
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(smem + addr));
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(smem + addr + 2048));
+  const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ float sigmoid_f(float g) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
+
+// Epilogue from the accumulators (lane: row 16 i + l % 16, columns 16 j +
+// 4 (l / 16) .. + 3 of the wave's block), 8-byte stores.
+template <Bwd kMode>
+__device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16], const BwdArgs& p,
+                                             const TileInfo& t, int wm, int wn) {
+  constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16;
+  const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int row_l = el & 15;
+  const int col_l = 4 * (el >> 4);
+  const int n0 = t.nt * BwdCfg::BN + wn * BwdCfg::WN + col_l;
+#pragma unroll
+  for (int i = 0; i < MT16; ++i) {
+    const int gm = wm * BwdCfg::WM + i * 16 + row_l;
+    int64_t row_off;
+    bool row_ok;
+    if constexpr (kMode == Bwd::kWgrad) {
+      const int m = t.mt * BwdCfg::BM + gm;
+      row_ok = m < p.M;
+      row_off = ((int64_t)t.e * p.M + min(m, p.M - 1)) * p.N;
+    } else {
+      row_ok = gm < t.rows;
+      row_off = (int64_t)(t.row0 + min(gm, t.rows - 1)) * p.N;
+    }
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) {
+      const int n = n0 + j * 16;
+      if (!row_ok || n >= p.N) continue;
+      const int64_t off = row_off + n;
+      bf16x4_t o0;
+      if constexpr (kMode == Bwd::kDgradDown) {
+        const bf16x4_t g4 = *reinterpret_cast<const bf16x4_t*>(p.e0 + off);
+        const bf16x4_t u4 = *reinterpret_cast<const bf16x4_t*>(p.e1 + off);
+        bf16x4_t o1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float dh = (float)(__bf16)acc[i][j][r];
+          const float g = (float)g4[r];
+          const float u = (float)u4[r];
+          const float s = sigmoid_f(g);
+          const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
+          o1[r] = (__bf16)(dh * act);                 // du
+          const float dact = (float)(__bf16)(dh * u);
+          o0[r] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
+        }
+        *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
+        *reinterpret_cast<bf16x4_t*>(p.c1 + off) = o1;
+      } else if (kMode == Bwd::kDgradIn && p.e0 != nullptr) {
+        const bf16x4_t add = *reinterpret_cast<const bf16x4_t*>(p.e0 + off);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o0[r] = (__bf16)((float)(__bf16)acc[i][j][r] + (float)add[r]);
+        *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o0[r] = (__bf16)acc[i][j][r];
+        *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
+      }
+    }
+  }
+}
+
+template <Bwd kMode>
+__global__ __launch_bounds__(BwdCfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs p) {
+  using Cfg = BwdCfg;
+  using Walk = std::conditional_t<kMode == Bwd::kWgrad, ExpertWalk, RowTileWalk>;
+  constexpr bool kAMn = kMode == Bwd::kWgrad;  // A operand MN-major (B always is)
+  __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
+
+  const Walk walk(p);
+  TileInfo t;
+  int logical = walk.seek(walk.first_slot(), t);
+  if (logical >= walk.total) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+
+  // Step protocol as in the prefill forward kernel: barrier X_g means every
+  // matrix-core wave has read step g and A(g + 1), B(g + 1) have landed;
+  // after it the DMA waves load A(g + 2) into A-buffer g % 2 and B(g + 3)
+  // into B-buffer g % 3.
+  if (wave >= Cfg::MW) {
+    const int dw = wave - Cfg::MW;
+    BwdCursor<kMode, Walk> ca, cb;
+    ca.start(p, logical, t);
+    cb.start(p, logical, t);
+    auto issue_a = [&](int buf) {
+      char* base = smem + Cfg::A_OFF + buf * Cfg::A_BYTES;
+#pragma unroll
+      for (int i = 0; i < Cfg::OPS; ++i) {
+        const int q = dw * Cfg::OPS + i;
+        ca.src.dma_a(p, lane, ca.kt, q, base + q * 1024);
+      }
+      ca.advance(p, walk);
+    };
+    auto issue_b = [&](int buf) {
+      char* base = smem + Cfg::B_OFF + buf * Cfg::B_BYTES;
+#pragma unroll
+      for (int i = 0; i < Cfg::OPS; ++i) {
+        const int q = dw * Cfg::OPS + i;
+        cb.src.dma_b(p, lane, cb.kt, q, base + q * 1024);
+      }
+      cb.advance(p, walk);
+    };
+    int a_iss = 0, b_iss = 0;
+    issue_b(0), ++b_iss;
+    issue_a(0), ++a_iss;
+    if (cb.live) issue_b(1), ++b_iss;
+    if (ca.live) issue_a(1), ++a_iss;
+    if (cb.live) issue_b(2), ++b_iss;
+    wait_groups<Cfg::OPS, 3>((a_iss - 1) + (b_iss - 1));  // A0 and B0 landed
+    __builtin_amdgcn_s_barrier();                          // X_{-1}
+    for (int g = 0;; ++g) {
+      wait_groups<Cfg::OPS, 1>(b_iss > g + 2 ? 1 : 0);
+      __builtin_amdgcn_s_barrier();  // X_g
+      const bool more = ca.live;
+      if (ca.live) issue_a(g & 1), ++a_iss;
+      if (cb.live) issue_b(g % 3), ++b_iss;
+      if (!more && g + 1 >= a_iss) break;
+    }
+    return;
+  }
+
+  // ---------------- matrix-core waves ----------------
+  const int wm = wave / Cfg::WGN;
+  const int wn = wave % Cfg::WGN;
+  constexpr int MT16 = Cfg::WM / 16, NT16 = Cfg::WN / 16;
+  constexpr int AR = Cfg::AR, PD = Cfg::PD, RG = Cfg::RG;
+  const int grp = lane >> 4;
+  const int gl = lane & 15;
+  // MN-major fragment bases: K-row 8 grp + (gl >> 2), bytes 8 (gl & 3) of
+  // the lane's 32-byte segment, segment bits swizzled by z = z(K-row).
+  const uint32_t mn_z = (uint32_t)((gl >> 2) | ((grp & 1) << 2));
+  const uint32_t mn_lane = (uint32_t)(8 * grp + (gl >> 2)) * Cfg::MN_ROW + 8u * (uint32_t)(gl & 3);
+  uint32_t vA, vB;
+  if constexpr (kAMn) {
+    vA = (uint32_t)Cfg::A_OFF + mn_lane + (uint32_t)wm * 256u + (mn_z << 5);
+  } else {
+    const int frag_row = lane & 15;
+    const int fq = lane >> 4;
+    const uint32_t v_lane = frag_row * kRowBytes + ((fq ^ ((frag_row >> 1) & 7)) << 4);
+    vA = (uint32_t)Cfg::A_OFF + (uint32_t)(wm * Cfg::WM) * kRowBytes + v_lane;
+  }
+  vB = (uint32_t)Cfg::B_OFF + mn_lane + (uint32_t)(wn >> 1) * 256u + ((mn_z ^ (4u * (uint32_t)(wn & 1))) << 5);
+  constexpr uint32_t kBEnd = (uint32_t)Cfg::LDS;
+  auto next_b = [&](uint32_t v) -> uint32_t {
+    const uint32_t n = v + Cfg::B_BYTES;
+    return n >= kBEnd ? n - Cfg::B_STAGES * Cfg::B_BYTES : n;
+  };
+  auto rotate = [&]() {
+    vA ^= (uint32_t)Cfg::A_BYTES;
+    vB = next_b(vB);
+    asm volatile("" : "+v"(vA), "+v"(vB));
+  };
+  bf16x8_t fa[AR], fb[NT16];
+  f32x4_t acc[MT16][NT16];
+  auto rdA = [&](uint32_t base, int kh, int i) -> bf16x8_t {
+    if constexpr (kAMn) {
+      return lds_tr_pair(smem, (base ^ ((uint32_t)i << 5)) + (uint32_t)kh * 32u * Cfg::MN_ROW);
+    } else {
+      return *reinterpret_cast<const bf16x8_t*>(smem + ((base ^ (kh ? 64u : 0u)) + i * 16 * kRowBytes));
+    }
+  };
+  auto rdB = [&](uint32_t base, int kh, int j) -> bf16x8_t {
+    return lds_tr_pair(smem, (base ^ ((uint32_t)j << 5)) + (uint32_t)kh * 32u * Cfg::MN_ROW);
+  };
+  auto step = [&]() {
+    uint32_t nA = 0, nB = 0;
+    static_for<16 / RG>([&](auto gg) {
+      constexpr int r0 = decltype(gg)::value * RG;
+      if constexpr (r0 + PD >= 16 && r0 + PD < 16 + RG) {
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();  // X_g
+        __builtin_amdgcn_sched_barrier(0);
+        nA = vA ^ (uint32_t)Cfg::A_BYTES;
+        nB = next_b(vB);
+      }
+      static_for<RG>([&](auto qq) {
+        constexpr int rp = r0 + PD + decltype(qq)::value;
+        if constexpr (rp < 16) {
+          fa[rp % AR] = rdA(vA, rp / 8, rp % 8);
+        } else {
+          fa[rp % AR] = rdA(nA, 0, rp - 16);
+        }
+      });
+#pragma unroll
+      for (int j = 0; j < NT16; ++j) {
+        static_for<RG>([&](auto qq) {
+          constexpr int r = r0 + decltype(qq)::value;
+          acc[r % 8][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[j], fa[r % AR], acc[r % 8][j], 0, 0, 0);
+        });
+        if constexpr (r0 + RG == 8) fb[j] = rdB(vB, 1, j);
+        if constexpr (r0 + RG == 16) fb[j] = rdB(nB, 0, j);
+      }
+    });
+  };
+
+  lds_barrier();  // X_{-1}
+#pragma unroll
+  for (int j = 0; j < NT16; ++j) fb[j] = rdB(vB, 0, j);
+#pragma unroll
+  for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < MT16; ++i)
+#pragma unroll
+      for (int j = 0; j < NT16; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
+    // every step, a tile's last included, prefetches the next step's first
+    // fragments (the next tile's); one loop body, one register assignment
+    for (int kt = 0; kt < t.ksteps; ++kt) {
+      step();
+      rotate();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    bwd_epilogue<kMode>(acc, p, t, wm, wn);
+    logical = walk.seek(logical + walk.G, t);
+    if (logical >= walk.total) break;
+  }
+}
+
+// One wave per permuted row r (token tok = sorted_token[r], routing weight
+// w): dy[r] = dout[tok] * w (bf16 product, mlp.py:97's y * w differentiated
+// in y) and dw[r] = sum_d bf16(dout[tok, d] * y[r, d]) (in w), y being the
+// unweighted expert output.
+__global__ __launch_bounds__(256) void row_grad_kernel(const bf16_t* __restrict__ dout,
+                                                       const int32_t* __restrict__ sorted_token,
+                                                       const bf16_t* __restrict__ sorted_w,
+                                                       const bf16_t* __restrict__ y, int64_t n_rows, int64_t dim,
+                                                       bf16_t* __restrict__ dy, bf16_t* __restrict__ dw_rows) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= n_rows) return;
+  const int64_t tok = sorted_token[r];
+  const float w = bf16_bits_to_f32(sorted_w[r]);
+  const bf16x8_t* src = reinterpret_cast<const bf16x8_t*>(dout + tok * dim);
+  const bf16x8_t* yr = reinterpret_cast<const bf16x8_t*>(y + r * dim);
+  bf16x8_t* dst = reinterpret_cast<bf16x8_t*>(dy + r * dim);
+  float acc = 0.0f;
+  for (int64_t v = lane; v < dim / 8; v += 64) {
+    const bf16x8_t d8 = src[v];
+    const bf16x8_t y8 = yr[v];
+    bf16x8_t o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float d = (float)d8[k];
+      o[k] = (__bf16)(d * w);
+      acc += (float)(__bf16)(d * (float)y8[k]);
+    }
+    dst[v] = o;
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) acc += __shfl_xor(acc, s, 64);
+  if (lane == 0) dw_rows[r] = f32_to_bf16_bits(acc);
+}
+
+template <Bwd kMode>
+int launch_bwd(const BwdArgs& p, int64_t total, hipStream_t s, const char* name) {
+  if (total == 0) return ASTRAI_MOE_OK;
+  if (total >= (1ll << 31)) return fail(ASTRAI_MOE_EINVAL, "%s: %lld tiles exceed the tile-index range", name,
+                                        (long long)total);
+  const int64_t grid = std::min<int64_t>(total, cu_count());
+  hipLaunchKernelGGL((gemm_bwd_kernel<kMode>), dim3((unsigned)grid), dim3(BwdCfg::THREADS), 0, s, p);
+  return check_launch(name);
+}
+
+}  // namespace
+
+int launch_row_grad(const void* dout, const int32_t* sorted_token, const void* sorted_w, const void* y,
+                    int64_t n_rows, int64_t dim, void* dy, void* dw_rows, hipStream_t s) {
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  hipLaunchKernelGGL(row_grad_kernel, dim3((unsigned)ceil_div(n_rows, 4)), dim3(256), 0, s,
+                     static_cast<const bf16_t*>(dout), sorted_token, static_cast<const bf16_t*>(sorted_w),
+                     static_cast<const bf16_t*>(y), n_rows, dim, static_cast<bf16_t*>(dy),
+                     static_cast<bf16_t*>(dw_rows));
+  return check_launch("row_grad_kernel");
+}
+
+int launch_dgrad_down(const void* dy, const int32_t* tiles, int64_t capacity, const void* const* w_down,
+                      const void* g, const void* u, int64_t dim, int64_t dim_ffn, void* dg, void* du,
+                      hipStream_t s) {
+  BwdArgs p{};
+  p.a0 = static_cast<const bf16_t*>(dy);
+  p.w0 = w_down;
+  p.tiles = tiles;
+  p.e0 = static_cast<const bf16_t*>(g);
+  p.e1 = static_cast<const bf16_t*>(u);
+  p.c0 = static_cast<bf16_t*>(dg);
+  p.c1 = static_cast<bf16_t*>(du);
+  p.K = (int)dim;
+  p.N = (int)dim_ffn;
+  p.n_tiles_n = (int)ceil_div(dim_ffn, BwdCfg::BN);
+  p.capacity = (int)capacity;
+  return launch_bwd<Bwd::kDgradDown>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_down>");
+}
+
+int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity, const void* const* w, int64_t k,
+                    int64_t n, const void* add, void* dx, hipStream_t s) {
+  BwdArgs p{};
+  p.a0 = static_cast<const bf16_t*>(d);
+  p.w0 = w;
+  p.tiles = tiles;
+  p.e0 = static_cast<const bf16_t*>(add);
+  p.c0 = static_cast<bf16_t*>(dx);
+  p.K = (int)k;
+  p.N = (int)n;
+  p.n_tiles_n = (int)ceil_div(n, BwdCfg::BN);
+  p.capacity = (int)capacity;
+  return launch_bwd<Bwd::kDgradIn>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in>");
+}
+
+int launch_wgrad(const void* a, const void* b, const int32_t* offsets, int n_experts, int64_t m, int64_t n,
+                 void* dw, hipStream_t s) {
+  BwdArgs p{};
+  p.a0 = static_cast<const bf16_t*>(a);
+  p.b_act = static_cast<const bf16_t*>(b);
+  p.offsets = offsets;
+  p.c0 = static_cast<bf16_t*>(dw);
+  p.M = (int)m;
+  p.N = (int)n;
+  p.n_tiles_m = (int)ceil_div(m, BwdCfg::BM);
+  p.n_tiles_n = (int)ceil_div(n, BwdCfg::BN);
+  p.n_experts = n_experts;
+  return launch_bwd<Bwd::kWgrad>(p, (int64_t)n_experts * p.n_tiles_m * p.n_tiles_n, s, "gemm_bwd_kernel<wgrad>");
+}
+
+}  // namespace astrai_moe

@@ -62,111 +62,10 @@
 //
 // Accumulator layout (16x16x32 with operands (W, A)): lane l, element r of
 // tile (i, j) is output row 16 i + l % 16, column 16 j + 4 (l / 16) + r.
-#include "moe_gemm.h"
-
-#include <algorithm>
-#include <atomic>
-#include <utility>
+#include "mfma_tile.h"
 
 namespace astrai_moe {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kBK = 64;             // K elements per stage
-constexpr int kRowBytes = kBK * 2;  // 128 bytes per staged row
-constexpr int kXcds = 8;
-
-template <typename F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-  (f(std::integral_constant<int, Is>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-__device__ inline void lds_dma_16(const void* gsrc, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
-                                   (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
-}
-
-template <int N>
-__device__ inline void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Wait until at most min(pending, MAXP) groups of PER DMA ops are in flight.
-template <int PER, int MAXP>
-__device__ inline void wait_groups(int pending) {
-  if constexpr (MAXP <= 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (pending >= MAXP)
-      wait_vmcnt<MAXP * PER>();
-    else
-      wait_groups<PER, MAXP - 1>(pending);
-  }
-}
-
-__device__ inline void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }  // lgkmcnt(0)
-
-// Barriers are s_barrier after explicit waits: LDS-DMA completion is tracked
-// by vmcnt, so the waits are placed by hand rather than by a fence.
-__device__ inline void lds_barrier() {
-  wait_lds();
-  __builtin_amdgcn_s_barrier();
-}
-
-// The persistent tile walk. Round r takes logical tile r * G + slot, where
-// slot gives the workgroups of one XCD a contiguous range of logical tiles;
-// logical tiles walk GM row tiles for every column tile. Dead row tiles (past
-// the live count the tile list reports) are skipped.
-template <int GM>
-struct TileWalk {
-  int G, total, n_live, group_size, capacity;
-  __device__ TileWalk(const int32_t* tiles, int capacity_, int n_tiles_n)
-      : G((int)gridDim.x), total(capacity_ * n_tiles_n), n_live(min(tiles[0], tiles[2])),
-        group_size(GM * n_tiles_n), capacity(capacity_) {}
-  __device__ int first_slot() const {
-    const int bid = blockIdx.x;
-    return (G % kXcds == 0) ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
-  }
-  __device__ bool decode(int logical, int& mt, int& nt) const {
-    const int first_m = (logical / group_size) * GM;
-    const int gm = min(GM, capacity - first_m);
-    const int in_group = logical - (first_m / GM) * group_size;
-    mt = first_m + in_group % gm;
-    nt = in_group / gm;
-    return mt < n_live;
-  }
-  // the first live logical tile at or after `logical` in this workgroup's sequence (>= total: none)
-  __device__ int seek(int logical, int& mt, int& nt) const {
-    while (logical < total && !decode(logical, mt, nt)) logical += G;
-    return logical;
-  }
-};
-
-// One 8-row DMA group of a stage: lane l loads row (l >> 3) of the group and
-// physical chunk l & 7, which holds logical chunk (l & 7) ^ ((row >> 1) & 7).
-// The source offsets are 32-bit byte offsets from uniform bases.
-struct DmaLane {
-  uint32_t chk0, chk1;  // byte offsets of the lane's chunk in even / odd 8-row groups
-  int row;              // row within the 8-row group
-  __device__ DmaLane(int lane, int kstep) {
-    row = lane >> 3;
-    const uint32_t koff = (uint32_t)kstep * kRowBytes;
-    chk0 = (uint32_t)(((lane & 7) ^ ((row >> 1) & 7)) << 4) + koff;
-    chk1 = (uint32_t)(((lane & 7) ^ (((row >> 1) + 4) & 7)) << 4) + koff;
-  }
-  // (arithmetic select: q's parity may be a runtime value)
-  __device__ uint32_t chunk(int q) const {
-    const uint32_t m = 0u - (uint32_t)(q & 1);
-    return (chk0 & ~m) | (chk1 & m);
-  }
-};
 
 // Per-tile global bases: activation rows and the expert's weight rows. With
 // kPacked the expert's weight comes as a packed copy (pack_kernel): the BN
@@ -331,9 +230,13 @@ struct StreamCfg {
 // Epilogue straight from the accumulators: lane l holds 4 consecutive output
 // columns of one row per 16x16 tile, stored as one 8-byte write (rows of a
 // tile are written by 16 lanes at once; L2 merges the pieces of each line).
-template <bool kGateUp, int WM, int WN, int BN>
+// kSave (training forward) also stores what the backward needs, at C's
+// positions: the bf16 gate and up projections (S0, S1) for gate/up, the
+// unweighted bf16 expert output (S0) for down.
+template <bool kGateUp, int WM, int WN, int BN, bool kSave>
 __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 16], const bf16_t* row_w, bf16_t* C,
-                                                  int N, int wm, int wn, int t_row0, int t_rows, int t_nt) {
+                                                  int N, int wm, int wn, int t_row0, int t_rows, int t_nt,
+                                                  bf16_t* S0, bf16_t* S1) {
   constexpr int MT16 = WM / 16, NT16 = WN / 16;
   const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   const int row_l = el & 15;
@@ -349,20 +252,30 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
     bf16_t* crow = C + (int64_t)srow * N + n_base + col_l;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      bf16x4_t o;
+      bf16x4_t o, s0, s1;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (kGateUp) {
-          const float g = (float)(__bf16)acc[i][j][r];
-          const float u = (float)(__bf16)acc[i][j + NJ][r];
+          s0[r] = (__bf16)acc[i][j][r];
+          s1[r] = (__bf16)acc[i][j + NJ][r];
+          const float g = (float)s0[r];
+          const float u = (float)s1[r];
           const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
           const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
           o[r] = (__bf16)(u * sv);
         } else {
-          o[r] = (__bf16)((float)(__bf16)acc[i][j][r] * w);
+          s0[r] = (__bf16)acc[i][j][r];
+          o[r] = (__bf16)((float)s0[r] * w);
         }
       }
-      if (gm < t_rows) *reinterpret_cast<bf16x4_t*>(crow + j * 16) = o;
+      if (gm < t_rows) {
+        *reinterpret_cast<bf16x4_t*>(crow + j * 16) = o;
+        if constexpr (kSave) {
+          const int64_t off = (crow - C) + j * 16;
+          *reinterpret_cast<bf16x4_t*>(S0 + off) = s0;
+          if constexpr (kGateUp) *reinterpret_cast<bf16x4_t*>(S1 + off) = s1;
+        }
+      }
     }
   }
 }
@@ -391,11 +304,11 @@ struct StepCursor {
   }
 };
 
-template <bool kGateUp, bool kPacked>
+template <bool kGateUp, bool kPacked, bool kSave>
 __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
-    int capacity, bf16_t* __restrict__ C) {
+    int capacity, bf16_t* __restrict__ C, bf16_t* __restrict__ S0, bf16_t* __restrict__ S1) {
   using Cfg = StreamCfg<kGateUp>;
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
 
@@ -567,7 +480,8 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
       rotate();
     }
     __builtin_amdgcn_sched_barrier(0);
-    store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt);
+    store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN, kSave>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt, S0,
+                                                                 S1);
     logical = walk.seek(logical + walk.G, mt, nt);
     if (logical >= walk.total) break;
   }
@@ -749,42 +663,19 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
 using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8>;
 static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfmaBigBM, "prefill tile height");
 
-bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
-
-// Compute units of the current device (one persistent workgroup each).
-int cu_count() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n == 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
-// Grid of a persistent launch: one workgroup per compute unit (the LDS
-// footprint allows no more), each walking its share of the tile list.
-int persistent_grid(int64_t capacity, int64_t n_tiles_n, int64_t* grid) {
-  const int64_t total = capacity * n_tiles_n;
-  if (total >= (1ll << 31))
-    return fail(ASTRAI_MOE_EINVAL, "gemm: %lld tiles exceed the tile-index range", (long long)total);
-  *grid = std::min<int64_t>(total, cu_count());
-  return ASTRAI_MOE_OK;
-}
-
-template <bool kGateUp, bool kPacked>
+template <bool kGateUp, bool kPacked, bool kSave = false>
 int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
-                  const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s) {
+                  const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s, void* S0 = nullptr,
+                  void* S1 = nullptr) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   using Cfg = StreamCfg<kGateUp>;
   const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
+  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked, kSave>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
                      static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
-                     (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C));
+                     (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0),
+                     static_cast<bf16_t*>(S1));
   return check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>");
 }
 
@@ -842,6 +733,19 @@ int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity, cons
                      hipStream_t s) {
   return packed ? down_dispatch<true>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s)
                 : down_dispatch<false>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s);
+}
+
+int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
+                             const void* const* w_up, int64_t dim, int64_t dim_ffn, void* h, void* g, void* u,
+                             hipStream_t s) {
+  return launch_stream<true, false, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, g, u);
+}
+
+int launch_mfma_down_save(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
+                          const void* sorted_w, int64_t dim_ffn, int64_t dim, void* y, void* y_unweighted,
+                          hipStream_t s) {
+  return launch_stream<false, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
+                                           y_unweighted, nullptr);
 }
 
 int launch_pack(const void* w0, const void* w1, int64_t rows, int64_t k, bool gate_up, void* out, hipStream_t s) {

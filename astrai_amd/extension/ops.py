@@ -350,3 +350,106 @@ def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tens
     h = moe_gemm_gate_up(perm.x_perm, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m, packed=packed)
     y = moe_gemm_down(h, perm.tiles, w_down, perm.sorted_w, n_experts, dim, block_m, packed=packed)
     return moe_combine(y, perm.token_pos, shared)
+
+
+# -- training: forward that keeps g, u, y and the backward kernels ------------
+
+
+def backward_supported(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
+    """Whether the grouped backward kernels take this expert shape (bf16 and
+    the matrix-core shapes; they run on 256-row tile lists)."""
+    return packed_supported(dim, dim_ffn, dtype)
+
+
+TRAIN_BLOCK_M = 256
+
+
+def _lib_call(name: str, *args) -> None:
+    _check(getattr(loader.library(), name)(*args), name)
+
+
+def moe_gemm_gate_up_train(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                           n_experts: int, dim_ffn: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``h`` as ``moe_gemm_gate_up`` plus the bf16 gate and up projections
+    ``g, u`` the backward needs (256-row tile list)."""
+    _require_gpu(x_perm, "x_perm", 2)
+    code = _dtype_code(x_perm, "x_perm")
+    n_rows, dim = x_perm.shape
+    h, g, u = (torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device) for _ in range(3))
+    _lib_call("astrai_moe_gemm_gate_up_train", x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
+              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, h.data_ptr(), g.data_ptr(),
+              u.data_ptr(), _stream(x_perm))
+    return h, g, u
+
+
+def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
+                        n_experts: int, dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``y * w`` as ``moe_gemm_down`` plus the unweighted expert output."""
+    _require_gpu(h, "h", 2)
+    code = _dtype_code(h, "h")
+    n_rows, dim_ffn = h.shape
+    if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
+        raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    y, y_unw = (torch.empty(n_rows, dim, dtype=h.dtype, device=h.device) for _ in range(2))
+    _lib_call("astrai_moe_gemm_down_train", h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
+              sorted_w.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, TRAIN_BLOCK_M, y.data_ptr(),
+              y_unw.data_ptr(), _stream(h))
+    return y, y_unw
+
+
+def moe_row_grad(dout: torch.Tensor, sorted_token: torch.Tensor, sorted_w: torch.Tensor,
+                 y_unweighted: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per permuted row: ``dy = dout[token] * w`` and ``dw = sum(dout[token] * y)``
+    (the two factors of mlp.py:97's ``expert_output * weights``)."""
+    _require_gpu(dout, "dout", 2)
+    _require_gpu(y_unweighted, "y_unweighted", 2)
+    code = _dtype_code(dout, "dout")
+    n_rows, dim = y_unweighted.shape
+    dy = torch.empty(n_rows, dim, dtype=dout.dtype, device=dout.device)
+    dw = torch.empty(n_rows, dtype=dout.dtype, device=dout.device)
+    _lib_call("astrai_moe_row_grad", dout.data_ptr(), sorted_token.data_ptr(), sorted_w.data_ptr(),
+              y_unweighted.data_ptr(), code, n_rows, dim, dy.data_ptr(), dw.data_ptr(), _stream(dout))
+    return dy, dw
+
+
+def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, g: torch.Tensor,
+                        u: torch.Tensor, n_experts: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``dh = dy . W_down`` with the SwiGLU backward fused: returns ``(dg, du)``."""
+    _require_gpu(dy, "dy", 2)
+    code = _dtype_code(dy, "dy")
+    n_rows, dim = dy.shape
+    dim_ffn = g.shape[1]
+    dg, du = (torch.empty(n_rows, dim_ffn, dtype=dy.dtype, device=dy.device) for _ in range(2))
+    _lib_call("astrai_moe_gemm_dgrad_down", dy.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
+              g.data_ptr(), u.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, dg.data_ptr(),
+              du.data_ptr(), _stream(dy))
+    return dg, du
+
+
+def moe_gemm_dgrad_gate_up(dg: torch.Tensor, du: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor,
+                           w_up: torch.Tensor, n_experts: int, dim: int) -> torch.Tensor:
+    """``dx_perm = dg . W_gate + du . W_up`` per expert."""
+    _require_gpu(dg, "dg", 2)
+    code = _dtype_code(dg, "dg")
+    n_rows, dim_ffn = dg.shape
+    dx = torch.empty(n_rows, dim, dtype=dg.dtype, device=dg.device)
+    _lib_call("astrai_moe_gemm_dgrad_gate_up", dg.data_ptr(), du.data_ptr(), tiles.data_ptr(), tiles.numel(),
+              w_gate.data_ptr(), w_up.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, TRAIN_BLOCK_M,
+              dx.data_ptr(), _stream(dg))
+    return dx
+
+
+def moe_gemm_wgrad(a: torch.Tensor, b: torch.Tensor, expert_offsets: torch.Tensor, n_experts: int) -> torch.Tensor:
+    """``dw[e] = a[rows of e]^T . b[rows of e]`` as one ``[E, m, n]`` tensor;
+    experts without rows are left unwritten."""
+    _require_gpu(a, "a", 2)
+    _require_gpu(b, "b", 2)
+    code = _dtype_code(a, "a")
+    if a.shape[0] != b.shape[0]:
+        raise ValueError("a and b must have the same rows")
+    n_rows, m = a.shape
+    n = b.shape[1]
+    dw = torch.empty(n_experts, m, n, dtype=a.dtype, device=a.device)
+    _lib_call("astrai_moe_gemm_wgrad", a.data_ptr(), b.data_ptr(), expert_offsets.data_ptr(), code, n_rows,
+              n_experts, m, n, dw.data_ptr(), _stream(a))
+    return dw

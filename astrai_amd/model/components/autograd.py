@@ -1,11 +1,18 @@
-"""Autograd for the MoE layer: HIP kernels forward, recompute backward.
+"""Autograd for the MoE layer: HIP kernels forward and backward.
 
 The reference layer is plain torch, so autograd differentiates it op by op
 (``astrai/model/components/mlp.py:22-25, 64-100``). Here the forward runs on
-the HIP kernels; the backward recomputes each expert's SwiGLU with the same
-torch ops as ``mlp.py:22-25`` and lets autograd differentiate them (the
-recompute that gradient checkpointing would do anyway), so the gradient
-formulas and their rounding points are the reference's:
+the HIP kernels. For bf16 and the matrix-core shapes the backward runs on
+grouped HIP kernels too (``astrai_moe_row_grad``, ``astrai_moe_gemm_dgrad_*``,
+``astrai_moe_gemm_wgrad``): the training forward saves the gate and up
+projections ``g, u``, ``h`` and the unweighted expert output ``y``, and the
+backward evaluates the formulas autograd applies to mlp.py:22-25 and :97-98
+(per expert e: ``dy = dout[tok] * w``, ``dw = sum(dout[tok] * y)``,
+``dh = dy W_down``, ``du = dh silu(g)``, ``dg = silu'(g) (dh u)``,
+``dx = dg W_gate + du W_up``, ``dW_down = dy^T h``, ``dW_gate = dg^T x``,
+``dW_up = du^T x``). Other shapes and fp32 recompute each expert's SwiGLU
+with the same torch ops as ``mlp.py:22-25`` and let autograd differentiate
+them, so the gradient formulas and their rounding points are the reference's:
 
 * ``out.index_add_(0, tok, y * w)`` (``mlp.py:98``): the gradient reaching
   expert row r is ``dout[tok(r)]``; the row's output gets ``dout * w`` and its
@@ -16,8 +23,8 @@ formulas and their rounding points are the reference's:
 * experts without rows get no gradient (the reference skips them, so their
   ``.grad`` stays ``None`` there too).
 
-The expert GEMMs of the backward are per-expert library GEMMs (torch
-``F.linear``); the row gather/scatter runs on the HIP kernels.
+In the recompute path the expert GEMMs of the backward are per-expert library
+GEMMs (torch ``F.linear``); the row gather/scatter runs on the HIP kernels.
 """
 
 from __future__ import annotations
@@ -60,19 +67,31 @@ class RoutedExperts(torch.autograd.Function):
         n_tokens, dim = x.shape
         top_k = topk_idx.shape[1]
         tg, tu, td = tables
-        block_m = ops.select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
         route = ops.RouteResult(topk_idx, topk_w.contiguous(), chunk_hist)
+        ctx.n_experts = n_experts
+        ctx.hip = ops.backward_supported(dim, dim_ffn, x.dtype)
+        if ctx.hip:
+            perm = ops.moe_permute(route, x, n_experts, ops.TRAIN_BLOCK_M)
+            h, g, u = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn)
+            y, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_experts, dim)
+            out = ops.moe_combine(y, perm.token_pos)
+            ctx.tables = tables
+            ctx.save_for_backward(perm.x_perm, perm.sorted_token, perm.sorted_w, perm.token_pos,
+                                  perm.expert_offsets, perm.tiles, h, g, u, y_unw, *weights)
+            return out
+        block_m = ops.select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
         perm = ops.moe_permute(route, x, n_experts, block_m)
         h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn, block_m)
         y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_experts, dim, block_m)
         out = ops.moe_combine(y, perm.token_pos)
-        ctx.n_experts = n_experts
         ctx.save_for_backward(perm.x_perm, perm.sorted_token, perm.sorted_w, perm.token_pos, perm.expert_offsets,
                               *weights)
         return out
 
     @staticmethod
     def backward(ctx, dout):
+        if ctx.hip:
+            return RoutedExperts._backward_hip(ctx, dout.contiguous())
         x_perm, sorted_token, sorted_w, token_pos, offsets, *weights = ctx.saved_tensors
         n_experts = ctx.n_experts
         wg, wu, wd = weights[:n_experts], weights[n_experts:2 * n_experts], weights[2 * n_experts:]
@@ -99,6 +118,33 @@ class RoutedExperts(torch.autograd.Function):
         dw = dw_rows[token_pos.long()]
         return (dx, dw, None, None, None, None, *g_gate, *g_up, *g_down)
 
+    @staticmethod
+    def _backward_hip(ctx, dout):
+        x_perm, sorted_token, sorted_w, token_pos, offsets, tiles, h, g, u, y_unw, *_ = ctx.saved_tensors
+        n_experts = ctx.n_experts
+        tg, tu, td = ctx.tables
+        dim = x_perm.shape[1]
+        dy, dw_rows = ops.moe_row_grad(dout, sorted_token, sorted_w, y_unw)
+        dg, du = ops.moe_gemm_dgrad_down(dy, tiles, td, g, u, n_experts)
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx_perm = ops.moe_gemm_dgrad_gate_up(dg, du, tiles, tg, tu, n_experts, dim)
+            dx = ops.moe_combine(dx_perm, token_pos)
+        dw = dw_rows[token_pos.long()] if ctx.needs_input_grad[1] else None
+        none = [None] * n_experts
+        g_gate, g_up, g_down = list(none), list(none), list(none)
+        if any(ctx.needs_input_grad[6:]):
+            d_gate = ops.moe_gemm_wgrad(dg, x_perm, offsets, n_experts)
+            d_up = ops.moe_gemm_wgrad(du, x_perm, offsets, n_experts)
+            d_down = ops.moe_gemm_wgrad(dy, h, offsets, n_experts)
+            # one host sync, after every kernel is enqueued: experts without
+            # rows get no gradient, as in the reference
+            counts = (offsets[1:] - offsets[:-1]).tolist()
+            for e, c in enumerate(counts):
+                if c > 0:
+                    g_gate[e], g_up[e], g_down[e] = d_gate[e], d_up[e], d_down[e]
+        return (dx, dw, None, None, None, None, *g_gate, *g_up, *g_down)
+
 
 class DenseExpert(torch.autograd.Function):
     """One dense SwiGLU expert (mlp.py:22-25, the shared experts and ``MLP``):
@@ -107,13 +153,34 @@ class DenseExpert(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, tables, dim_ffn, wg, wu, wd):
         tg, tu, td = tables
+        n_tokens, dim = x.shape
+        ctx.hip = n_tokens > 0 and ops.backward_supported(dim, dim_ffn, x.dtype)
+        if ctx.hip:
+            tiles, ones = ops._dense_tiles(n_tokens, ops.TRAIN_BLOCK_M, x.device, x.dtype)
+            h, g, u = ops.moe_gemm_gate_up_train(x, tiles, tg, tu, 1, dim_ffn)
+            out = ops.moe_gemm_down(h, tiles, td, ones, 1, dim, ops.TRAIN_BLOCK_M)
+            ctx.tables = tables
+            ctx.save_for_backward(x, tiles, h, g, u, wg, wu, wd)
+            return out
         ctx.save_for_backward(x, wg, wu, wd)
         return ops.moe_dense_mlp(x, tg, tu, td, dim_ffn)
 
     @staticmethod
     def backward(ctx, dout):
+        dout = dout.contiguous()
+        if ctx.hip:
+            x, tiles, h, g, u, *_ = ctx.saved_tensors
+            tg, tu, td = ctx.tables
+            n_tokens, dim = x.shape
+            dg, du = ops.moe_gemm_dgrad_down(dout, tiles, td, g, u, 1)
+            dx = ops.moe_gemm_dgrad_gate_up(dg, du, tiles, tg, tu, 1, dim) if ctx.needs_input_grad[0] else None
+            offsets = torch.tensor([0, n_tokens], dtype=torch.int32, device=x.device)
+            gg = ops.moe_gemm_wgrad(dg, x, offsets, 1)[0]
+            gu = ops.moe_gemm_wgrad(du, x, offsets, 1)[0]
+            gd = ops.moe_gemm_wgrad(dout, h, offsets, 1)[0]
+            return dx, None, None, gg, gu, gd
         x, wg, wu, wd = ctx.saved_tensors
-        gx, gg, gu, gd = _expert_grads(x, wg, wu, wd, dout.contiguous())
+        gx, gg, gu, gd = _expert_grads(x, wg, wu, wd, dout)
         return gx, None, None, gg, gu, gd
 
 

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 2
+#define ASTRAI_MOE_ABI_VERSION 3
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -220,6 +220,88 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
                        const void* shared, int n_shared, int dtype,
                        int64_t n_tokens, int top_k, int64_t dim, void* out,
                        void* stream);
+
+/*
+ * Training: forward that keeps what the backward needs, and the backward.
+ * The reference gets its gradients from torch autograd over mlp.py:22-25
+ * and :89-98; these entry points compute the same quantities with grouped
+ * kernels (bf16 only; dim % 256 == 0, dim_ffn % 128 == 0; tile lists built
+ * with block_m = 256). Per expert e with permuted rows R_e:
+ *
+ *   forward   g = x W_gate^T, u = x W_up^T, h = u * silu(g), y = h W_down^T,
+ *             out = sum over slots of y * w                    (mlp.py:22-24, :97-98)
+ *   backward  dy = dout[tok] * w,  dw = sum_d dout[tok] * y    (d of y * w)
+ *             du = dh * silu(g),  dg = silu'(g) * (dh * u),  dh = dy W_down
+ *             dx_perm = dg W_gate + du W_up,  dx = sum over slots (astrai_moe_combine)
+ *             dW_down[e] = dy^T h,  dW_gate[e] = dg^T x_perm,  dW_up[e] = du^T x_perm
+ *
+ * astrai_moe_gemm_gate_up_train: astrai_moe_gemm_gate_up plus g and u
+ *   ([n_rows, dim_ffn] bf16, the rounded projections silu and the product use).
+ * astrai_moe_gemm_down_train: astrai_moe_gemm_down plus y_unweighted
+ *   ([n_rows, dim] bf16, the rounded expert output before the routing weight).
+ */
+int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles,
+                                  int64_t tiles_len, const void* const* w_gate,
+                                  const void* const* w_up, int dtype,
+                                  int64_t n_rows, int n_experts, int64_t dim,
+                                  int64_t dim_ffn, int block_m, void* h,
+                                  void* g, void* u, void* stream);
+int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles,
+                               int64_t tiles_len, const void* const* w_down,
+                               const void* sorted_w, int dtype, int64_t n_rows,
+                               int n_experts, int64_t dim_ffn, int64_t dim,
+                               int block_m, void* y, void* y_unweighted,
+                               void* stream);
+
+/*
+ * Per permuted row r (token sorted_token[r], weight sorted_w[r]):
+ *   dy[r]      = dout[token] * w, rounded per element     [n_rows, dim] bf16
+ *   dw_rows[r] = sum_d bf16(dout[token, d] * y[r, d])     [n_rows] bf16
+ * (mlp.py:97's expert_output * weights, differentiated in both factors).
+ */
+int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token,
+                        const void* sorted_w, const void* y_unweighted,
+                        int dtype, int64_t n_rows, int64_t dim, void* dy,
+                        void* dw_rows, void* stream);
+
+/*
+ * Grouped dgrad of the down projection with the SwiGLU backward fused:
+ *   dh = dy . W_down[e] (W_down [dim, dim_ffn]), rounded to bf16, then
+ *   du = bf16(dh * silu(g)), dg = bf16(bf16(dh * u) * silu'(g))
+ * (the order torch autograd takes through mlp.py:23).
+ *   dy [n_rows, dim], g, u, dg, du [n_rows, dim_ffn], all bf16.
+ */
+int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles,
+                               int64_t tiles_len, const void* const* w_down,
+                               const void* g, const void* u, int dtype,
+                               int64_t n_rows, int n_experts, int64_t dim,
+                               int64_t dim_ffn, int block_m, void* dg, void* du,
+                               void* stream);
+
+/*
+ * Grouped dgrad of the gate and up projections:
+ *   dx_perm = bf16(bf16(dg . W_gate[e]) + bf16(du . W_up[e]))   [n_rows, dim] bf16
+ * (autograd's rounding: each linear's input gradient, then their sum).
+ */
+int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du,
+                                  const int32_t* tiles, int64_t tiles_len,
+                                  const void* const* w_gate,
+                                  const void* const* w_up, int dtype,
+                                  int64_t n_rows, int n_experts,
+                                  int64_t dim_ffn, int64_t dim, int block_m,
+                                  void* dx_perm, void* stream);
+
+/*
+ * Per-expert weight gradient: dw[e] = a[rows of e]^T . b[rows of e], the rows
+ * of expert e being expert_offsets[e] .. expert_offsets[e + 1] - 1.
+ *   a [n_rows, m], b [n_rows, n], dw [n_experts, m, n], all bf16 (m % 8 == 0,
+ *   n % 8 == 0). Experts without rows are not written.
+ * dW_down: (a, b) = (dy, h); dW_gate: (dg, x_perm); dW_up: (du, x_perm).
+ */
+int astrai_moe_gemm_wgrad(const void* a, const void* b,
+                          const int32_t* expert_offsets, int dtype,
+                          int64_t n_rows, int n_experts, int64_t m, int64_t n,
+                          void* dw, void* stream);
 
 #ifdef __cplusplus
 }

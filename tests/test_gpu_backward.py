@@ -121,12 +121,13 @@ def test_moe_backward(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, bias):
     _check_moe(layer, x, f"d{dim}_f{dim_ffn}_e{n_exp}_s{n_shared}_k{top_k}_{dtype}")
 
 
-def test_moe_backward_empty_experts(gpu):
+@pytest.mark.parametrize("dim", [128, 256])  # recompute backward / grouped backward kernels
+def test_moe_backward_empty_experts(gpu, dim):
     # a sharp router leaves most of the 32 experts without tokens
-    layer = _random_layer(gpu, 128, 256, 32, 0, 2, torch.bfloat16, router_scale=40.0, bias=True)
+    layer = _random_layer(gpu, dim, 256, 32, 0, 2, torch.bfloat16, router_scale=40.0, bias=True)
     with torch.no_grad():
         layer.router.bias.copy_(torch.linspace(-30.0, 30.0, 32, device=gpu))
-    x = torch.randn(1, 40, 128, device=gpu).to(torch.bfloat16)
+    x = torch.randn(1, 40, dim, device=gpu).to(torch.bfloat16)
     n_none = _check_moe(layer, x, "empty experts")
     assert n_none >= 3 * 10
 
@@ -137,14 +138,15 @@ def test_moe_backward_workload_rows(gpu):
     _check_moe(layer, x, "d2048_f1408_e64_k6 t2048")
 
 
-def test_mlp_backward(gpu):
+@pytest.mark.parametrize("dim,dim_ffn", [(192, 320), (256, 384)])  # recompute / grouped backward kernels
+def test_mlp_backward(gpu, dim, dim_ffn):
     torch.manual_seed(1)
-    mlp = MLP(192, 320).to(device=gpu, dtype=torch.bfloat16)
+    mlp = MLP(dim, dim_ffn).to(device=gpu, dtype=torch.bfloat16)
     for m in mlp.modules():
         if hasattr(m, "reset_parameters"):
             m.reset_parameters()
-    x = torch.randn(3, 50, 192, device=gpu).to(torch.bfloat16)
-    dout = torch.randn(3, 50, 192, device=gpu).to(torch.bfloat16)
+    x = torch.randn(3, 50, dim, device=gpu).to(torch.bfloat16)
+    dout = torch.randn(3, 50, dim, device=gpu).to(torch.bfloat16)
     w = R.ExpertWeights(_leaf(mlp.gate.weight), _leaf(mlp.up.weight), _leaf(mlp.down.weight))
     xr = _leaf(x)
     R.expert_mlp(xr, w).backward(dout)
@@ -155,6 +157,23 @@ def test_mlp_backward(gpu):
     for name, got, want in (("gate", mlp.gate.weight.grad, w.gate.grad), ("up", mlp.up.weight.grad, w.up.grad),
                             ("down", mlp.down.weight.grad, w.down.grad)):
         _close(got, want, torch.bfloat16, f"mlp d{name}")
+
+
+def test_bf16_matrix_core_shapes_use_the_backward_kernels(gpu, monkeypatch):
+    from astrai_amd.extension import ops
+
+    calls = []
+    for name in ("moe_row_grad", "moe_gemm_dgrad_down", "moe_gemm_dgrad_gate_up", "moe_gemm_wgrad"):
+        fn = getattr(ops, name)
+        monkeypatch.setattr(ops, name, lambda *a, _fn=fn, _n=name, **k: (calls.append(_n), _fn(*a, **k))[1])
+    layer = _random_layer(gpu, 256, 256, 8, 1, 2, torch.bfloat16)
+    x = torch.randn(1, 300, 256, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    layer(x).sum().backward()
+    torch.cuda.synchronize()
+    # routed: row grad, 2 dgrad, 3 wgrad; shared: 2 dgrad, 3 wgrad
+    assert calls.count("moe_row_grad") == 1
+    assert calls.count("moe_gemm_wgrad") == 6
+    assert calls.count("moe_gemm_dgrad_down") == 2 and calls.count("moe_gemm_dgrad_gate_up") == 2
 
 
 def test_inference_mode_has_no_graph(gpu):
