@@ -32,12 +32,13 @@ int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
                      void* y, hipStream_t s);
 
 // Training forward (256-row tiles): as launch_mfma_gate_up / launch_mfma_down,
-// also storing the bf16 gate and up projections (g, u: [rows, dim_ffn]) or
-// the unweighted bf16 expert output (y_unweighted: [rows, dim]).
+// also storing the bf16 gate and up projections (gu: [rows, 2 dim_ffn],
+// blocks of 4 gate columns then the same 4 up columns) or the unweighted bf16
+// expert output (y_unweighted: [rows, dim]).
 int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles,
                              int64_t capacity, const void* const* w_gate,
                              const void* const* w_up, int64_t dim,
-                             int64_t dim_ffn, void* h, void* g, void* u,
+                             int64_t dim_ffn, void* h, void* gu,
                              hipStream_t s);
 int launch_mfma_down_save(const void* h, const int32_t* tiles,
                           int64_t capacity, const void* const* w_down,
@@ -50,11 +51,10 @@ int launch_row_grad(const void* dout, const int32_t* sorted_token,
                     const void* sorted_w, const void* y, int64_t n_rows,
                     int64_t dim, void* dy, void* dw_rows, hipStream_t s);
 // dg, du [rows, dim_ffn] from dy [rows, dim], W_down [dim, dim_ffn] and the
-// saved g, u;
+// saved interleaved gu;
 int launch_dgrad_down(const void* dy, const int32_t* tiles, int64_t capacity,
-                      const void* const* w_down, const void* g, const void* u,
-                      int64_t dim, int64_t dim_ffn, void* dg, void* du,
-                      hipStream_t s);
+                      const void* const* w_down, const void* gu, int64_t dim,
+                      int64_t dim_ffn, void* dg, void* du, hipStream_t s);
 // dx [rows, n] = bf16(d . W[e]) (+ add, rounded again), W[e] [k, n];
 int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity,
                     const void* const* w, int64_t k, int64_t n,

@@ -294,18 +294,18 @@ static int check_train(const char* who, int dtype, int64_t dim, int64_t dim_ffn,
 extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles, int64_t tiles_len,
                                              const void* const* w_gate, const void* const* w_up, int dtype,
                                              int64_t n_rows, int n_experts, int64_t dim, int64_t dim_ffn,
-                                             int block_m, void* h, void* g, void* u, void* stream) {
+                                             int block_m, void* h, void* gu, void* stream) {
   clear_error();
   int rc = check_common("gemm_gate_up_train", x_perm, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn,
                         block_m, h);
   if (rc) return rc;
   if ((rc = check_train("gemm_gate_up_train", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
-  ASTRAI_REQUIRE(w_gate && w_up && g && u, "gemm_gate_up_train: null weight table or output");
-  ASTRAI_REQUIRE(aligned16_ptr(x_perm) && aligned16_ptr(h) && aligned16_ptr(g) && aligned16_ptr(u),
+  ASTRAI_REQUIRE(w_gate && w_up && gu, "gemm_gate_up_train: null weight table or output");
+  ASTRAI_REQUIRE(aligned16_ptr(x_perm) && aligned16_ptr(h) && aligned16_ptr(gu),
                  "gemm_gate_up_train: buffers must be 16-byte aligned");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
-  return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, g, u,
+  return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, gu,
                                   static_cast<hipStream_t>(stream));
 }
 
@@ -342,21 +342,20 @@ extern "C" int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token
 }
 
 extern "C" int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles, int64_t tiles_len,
-                                          const void* const* w_down, const void* g, const void* u, int dtype,
-                                          int64_t n_rows, int n_experts, int64_t dim, int64_t dim_ffn, int block_m,
-                                          void* dg, void* du, void* stream) {
+                                          const void* const* w_down, const void* gu, int dtype, int64_t n_rows,
+                                          int n_experts, int64_t dim, int64_t dim_ffn, int block_m, void* dg,
+                                          void* du, void* stream) {
   clear_error();
   int rc = check_common("gemm_dgrad_down", dy, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn, block_m,
                         dg);
   if (rc) return rc;
   if ((rc = check_train("gemm_dgrad_down", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
-  ASTRAI_REQUIRE(w_down && g && u && du, "gemm_dgrad_down: null weight table or buffer");
-  ASTRAI_REQUIRE(aligned16_ptr(dy) && aligned16_ptr(g) && aligned16_ptr(u) && aligned16_ptr(dg) &&
-                     aligned16_ptr(du),
+  ASTRAI_REQUIRE(w_down && gu && du, "gemm_dgrad_down: null weight table or buffer");
+  ASTRAI_REQUIRE(aligned16_ptr(dy) && aligned16_ptr(gu) && aligned16_ptr(dg) && aligned16_ptr(du),
                  "gemm_dgrad_down: buffers must be 16-byte aligned");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
-  return launch_dgrad_down(dy, tiles, capacity, w_down, g, u, dim, dim_ffn, dg, du, static_cast<hipStream_t>(stream));
+  return launch_dgrad_down(dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, const int32_t* tiles, int64_t tiles_len,

@@ -11,8 +11,8 @@
 //          the second adding the first's result in its epilogue (autograd
 //          rounds each linear's input gradient, then their sum)
 //   dW_down = dy^T . h,  dW_gate = dg^T . x,  dW_up = du^T . x   (wgrad)
-// with g, u the bf16 gate / up projections and h = u * silu(g) saved by the
-// training forward.
+// with g, u the bf16 gate / up projections (saved interleaved, 4 columns of g
+// then the same 4 of u) and h = u * silu(g) saved by the training forward.
 //
 // Operand layouts. The forward kernels read both operands K-contiguous. Here
 // the dgrad weight operand (W_down [K = D, N = F], W_gate/W_up [K = F, N = D])
@@ -51,7 +51,7 @@ namespace {
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x8_t __attribute__((ext_vector_type(8)));
 
-enum class Bwd { kDgradDown, kDgradIn, kWgrad };
+enum class Bwd { kDgradDown, kDgradIn, kDgradInAdd, kWgrad };
 
 // Source of K-rows past an expert's last row in wgrad (zero contribution).
 __device__ __attribute__((aligned(512))) uint4 g_zero_row[32] = {};
@@ -62,8 +62,7 @@ struct BwdArgs {
   const bf16_t* b_act;       // wgrad: B [rows, N]
   const int32_t* tiles;      // dgrad: 256-row tile list
   const int32_t* offsets;    // wgrad: expert row offsets [E + 1]
-  const bf16_t* e0;          // dgrad down epilogue: g [rows, N]; dgrad in: addend or null
-  const bf16_t* e1;          // dgrad down epilogue: u [rows, N]
+  const bf16_t* e0;          // dgrad down epilogue: gu [rows, 2 N]; dgrad in: addend or null
   bf16_t* c0;                // dgrad down: dg; dgrad in: dx; wgrad: dW [E, M, N]
   bf16_t* c1;                // dgrad down: du
   int K;                     // dgrad: K
@@ -274,14 +273,13 @@ __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][Bwd
       const int64_t off = row_off + n;
       bf16x4_t o0;
       if constexpr (kMode == Bwd::kDgradDown) {
-        const bf16x4_t g4 = *reinterpret_cast<const bf16x4_t*>(p.e0 + off);
-        const bf16x4_t u4 = *reinterpret_cast<const bf16x4_t*>(p.e1 + off);
+        const bf16x8_t gu = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off);
         bf16x4_t o1;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float dh = (float)(__bf16)acc[i][j][r];
-          const float g = (float)g4[r];
-          const float u = (float)u4[r];
+          const float g = (float)gu[r];
+          const float u = (float)gu[4 + r];
           const float s = sigmoid_f(g);
           const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
           o1[r] = (__bf16)(dh * act);                 // du
@@ -290,7 +288,7 @@ __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][Bwd
         }
         *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
         *reinterpret_cast<bf16x4_t*>(p.c1 + off) = o1;
-      } else if (kMode == Bwd::kDgradIn && p.e0 != nullptr) {
+      } else if constexpr (kMode == Bwd::kDgradInAdd) {
         const bf16x4_t add = *reinterpret_cast<const bf16x4_t*>(p.e0 + off);
 #pragma unroll
         for (int r = 0; r < 4; ++r) o0[r] = (__bf16)((float)(__bf16)acc[i][j][r] + (float)add[r]);
@@ -522,14 +520,12 @@ int launch_row_grad(const void* dout, const int32_t* sorted_token, const void* s
 }
 
 int launch_dgrad_down(const void* dy, const int32_t* tiles, int64_t capacity, const void* const* w_down,
-                      const void* g, const void* u, int64_t dim, int64_t dim_ffn, void* dg, void* du,
-                      hipStream_t s) {
+                      const void* gu, int64_t dim, int64_t dim_ffn, void* dg, void* du, hipStream_t s) {
   BwdArgs p{};
   p.a0 = static_cast<const bf16_t*>(dy);
   p.w0 = w_down;
   p.tiles = tiles;
-  p.e0 = static_cast<const bf16_t*>(g);
-  p.e1 = static_cast<const bf16_t*>(u);
+  p.e0 = static_cast<const bf16_t*>(gu);
   p.c0 = static_cast<bf16_t*>(dg);
   p.c1 = static_cast<bf16_t*>(du);
   p.K = (int)dim;
@@ -551,6 +547,8 @@ int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity, const
   p.N = (int)n;
   p.n_tiles_n = (int)ceil_div(n, BwdCfg::BN);
   p.capacity = (int)capacity;
+  if (add != nullptr)
+    return launch_bwd<Bwd::kDgradInAdd>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in_add>");
   return launch_bwd<Bwd::kDgradIn>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in>");
 }
 

@@ -230,9 +230,11 @@ struct StreamCfg {
 // Epilogue straight from the accumulators: lane l holds 4 consecutive output
 // columns of one row per 16x16 tile, stored as one 8-byte write (rows of a
 // tile are written by 16 lanes at once; L2 merges the pieces of each line).
-// kSave (training forward) also stores what the backward needs, at C's
-// positions: the bf16 gate and up projections (S0, S1) for gate/up, the
-// unweighted bf16 expert output (S0) for down.
+// kSave (training forward) also stores what the backward needs: for gate/up
+// the bf16 gate and up projections interleaved in blocks of 4 columns (S0
+// [rows, 2 N]: g[c..c+3] then u[c..c+3] at 2 c, one 16-byte store per lane,
+// so each wave completes whole 128-byte lines), for down the unweighted bf16
+// expert output (S0, at C's positions).
 template <bool kGateUp, int WM, int WN, int BN, bool kSave>
 __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 16], const bf16_t* row_w, bf16_t* C,
                                                   int N, int wm, int wn, int t_row0, int t_rows, int t_nt,
@@ -272,8 +274,14 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
         *reinterpret_cast<bf16x4_t*>(crow + j * 16) = o;
         if constexpr (kSave) {
           const int64_t off = (crow - C) + j * 16;
-          *reinterpret_cast<bf16x4_t*>(S0 + off) = s0;
-          if constexpr (kGateUp) *reinterpret_cast<bf16x4_t*>(S1 + off) = s1;
+          if constexpr (kGateUp) {
+            bf16x8_t gu;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) gu[r] = s0[r], gu[4 + r] = s1[r];
+            *reinterpret_cast<bf16x8_t*>(S0 + 2 * off) = gu;  // row r, column c of h -> 2 (r N + c)
+          } else {
+            *reinterpret_cast<bf16x4_t*>(S0 + off) = s0;
+          }
         }
       }
     }
@@ -736,9 +744,10 @@ int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity, cons
 }
 
 int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
-                             const void* const* w_up, int64_t dim, int64_t dim_ffn, void* h, void* g, void* u,
+                             const void* const* w_up, int64_t dim, int64_t dim_ffn, void* h, void* gu,
                              hipStream_t s) {
-  return launch_stream<true, false, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, g, u);
+  return launch_stream<true, false, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, gu,
+                                          nullptr);
 }
 
 int launch_mfma_down_save(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,

@@ -57,11 +57,11 @@ _SIGNATURES: dict[str, tuple] = {
     "astrai_moe_gemm_gate_up_packed": (_int, [_vp, _vp, _i64, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp]),
     "astrai_moe_gemm_down_packed": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp]),
     "astrai_moe_gemm_gate_up_train": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp,
-                                             _vp, _vp]),
+                                             _vp]),
     "astrai_moe_gemm_down_train": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp,
                                           _vp]),
     "astrai_moe_row_grad": (_int, [_vp, _vp, _vp, _vp, _int, _i64, _i64, _vp, _vp, _vp]),
-    "astrai_moe_gemm_dgrad_down": (_int, [_vp, _vp, _i64, _vp, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp,
+    "astrai_moe_gemm_dgrad_down": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp,
                                           _vp]),
     "astrai_moe_gemm_dgrad_gate_up": (_int, [_vp, _vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp,
                                              _vp]),

@@ -369,17 +369,26 @@ def _lib_call(name: str, *args) -> None:
 
 
 def moe_gemm_gate_up_train(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
-                           n_experts: int, dim_ffn: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """``h`` as ``moe_gemm_gate_up`` plus the bf16 gate and up projections
-    ``g, u`` the backward needs (256-row tile list)."""
+                           n_experts: int, dim_ffn: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``h`` as ``moe_gemm_gate_up`` plus ``gu [rows, 2 * dim_ffn]``, the bf16
+    gate and up projections the backward needs, interleaved per 4 columns
+    (``gu_split`` separates them); 256-row tile list."""
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
-    h, g, u = (torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device) for _ in range(3))
+    h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
+    gu = torch.empty(n_rows, 2 * dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     _lib_call("astrai_moe_gemm_gate_up_train", x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
-              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, h.data_ptr(), g.data_ptr(),
-              u.data_ptr(), _stream(x_perm))
-    return h, g, u
+              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, h.data_ptr(), gu.data_ptr(),
+              _stream(x_perm))
+    return h, gu
+
+
+def gu_split(gu: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(g, u)`` views of the interleaved projections of ``moe_gemm_gate_up_train``."""
+    rows, two_f = gu.shape
+    v = gu.view(rows, two_f // 8, 2, 4)
+    return v[:, :, 0, :].reshape(rows, two_f // 2), v[:, :, 1, :].reshape(rows, two_f // 2)
 
 
 def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
@@ -412,17 +421,19 @@ def moe_row_grad(dout: torch.Tensor, sorted_token: torch.Tensor, sorted_w: torch
     return dy, dw
 
 
-def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, g: torch.Tensor,
-                        u: torch.Tensor, n_experts: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """``dh = dy . W_down`` with the SwiGLU backward fused: returns ``(dg, du)``."""
+def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, gu: torch.Tensor,
+                        n_experts: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``dh = dy . W_down`` with the SwiGLU backward fused (``gu`` from
+    ``moe_gemm_gate_up_train``): returns ``(dg, du)``."""
     _require_gpu(dy, "dy", 2)
+    _require_gpu(gu, "gu", 2)
     code = _dtype_code(dy, "dy")
     n_rows, dim = dy.shape
-    dim_ffn = g.shape[1]
+    dim_ffn = gu.shape[1] // 2
     dg, du = (torch.empty(n_rows, dim_ffn, dtype=dy.dtype, device=dy.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_dgrad_down", dy.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
-              g.data_ptr(), u.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, dg.data_ptr(),
-              du.data_ptr(), _stream(dy))
+              gu.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, dg.data_ptr(), du.data_ptr(),
+              _stream(dy))
     return dg, du
 
 

@@ -5,7 +5,8 @@ The reference layer is plain torch, so autograd differentiates it op by op
 the HIP kernels. For bf16 and the matrix-core shapes the backward runs on
 grouped HIP kernels too (``astrai_moe_row_grad``, ``astrai_moe_gemm_dgrad_*``,
 ``astrai_moe_gemm_wgrad``): the training forward saves the gate and up
-projections ``g, u``, ``h`` and the unweighted expert output ``y``, and the
+projections ``g, u`` (interleaved), ``h`` and the unweighted expert output
+``y``, and the
 backward evaluates the formulas autograd applies to mlp.py:22-25 and :97-98
 (per expert e: ``dy = dout[tok] * w``, ``dw = sum(dout[tok] * y)``,
 ``dh = dy W_down``, ``du = dh silu(g)``, ``dg = silu'(g) (dh u)``,
@@ -72,12 +73,12 @@ class RoutedExperts(torch.autograd.Function):
         ctx.hip = ops.backward_supported(dim, dim_ffn, x.dtype)
         if ctx.hip:
             perm = ops.moe_permute(route, x, n_experts, ops.TRAIN_BLOCK_M)
-            h, g, u = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn)
+            h, gu = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn)
             y, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_experts, dim)
             out = ops.moe_combine(y, perm.token_pos)
             ctx.tables = tables
             ctx.save_for_backward(perm.x_perm, perm.sorted_token, perm.sorted_w, perm.token_pos,
-                                  perm.expert_offsets, perm.tiles, h, g, u, y_unw, *weights)
+                                  perm.expert_offsets, perm.tiles, h, gu, y_unw, *weights)
             return out
         block_m = ops.select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
         perm = ops.moe_permute(route, x, n_experts, block_m)
@@ -120,12 +121,12 @@ class RoutedExperts(torch.autograd.Function):
 
     @staticmethod
     def _backward_hip(ctx, dout):
-        x_perm, sorted_token, sorted_w, token_pos, offsets, tiles, h, g, u, y_unw, *_ = ctx.saved_tensors
+        x_perm, sorted_token, sorted_w, token_pos, offsets, tiles, h, gu, y_unw, *_ = ctx.saved_tensors
         n_experts = ctx.n_experts
         tg, tu, td = ctx.tables
         dim = x_perm.shape[1]
         dy, dw_rows = ops.moe_row_grad(dout, sorted_token, sorted_w, y_unw)
-        dg, du = ops.moe_gemm_dgrad_down(dy, tiles, td, g, u, n_experts)
+        dg, du = ops.moe_gemm_dgrad_down(dy, tiles, td, gu, n_experts)
         dx = None
         if ctx.needs_input_grad[0]:
             dx_perm = ops.moe_gemm_dgrad_gate_up(dg, du, tiles, tg, tu, n_experts, dim)
@@ -157,10 +158,10 @@ class DenseExpert(torch.autograd.Function):
         ctx.hip = n_tokens > 0 and ops.backward_supported(dim, dim_ffn, x.dtype)
         if ctx.hip:
             tiles, ones = ops._dense_tiles(n_tokens, ops.TRAIN_BLOCK_M, x.device, x.dtype)
-            h, g, u = ops.moe_gemm_gate_up_train(x, tiles, tg, tu, 1, dim_ffn)
+            h, gu = ops.moe_gemm_gate_up_train(x, tiles, tg, tu, 1, dim_ffn)
             out = ops.moe_gemm_down(h, tiles, td, ones, 1, dim, ops.TRAIN_BLOCK_M)
             ctx.tables = tables
-            ctx.save_for_backward(x, tiles, h, g, u, wg, wu, wd)
+            ctx.save_for_backward(x, tiles, h, gu, wg, wu, wd)
             return out
         ctx.save_for_backward(x, wg, wu, wd)
         return ops.moe_dense_mlp(x, tg, tu, td, dim_ffn)
@@ -169,10 +170,10 @@ class DenseExpert(torch.autograd.Function):
     def backward(ctx, dout):
         dout = dout.contiguous()
         if ctx.hip:
-            x, tiles, h, g, u, *_ = ctx.saved_tensors
+            x, tiles, h, gu, *_ = ctx.saved_tensors
             tg, tu, td = ctx.tables
             n_tokens, dim = x.shape
-            dg, du = ops.moe_gemm_dgrad_down(dout, tiles, td, g, u, 1)
+            dg, du = ops.moe_gemm_dgrad_down(dout, tiles, td, gu, 1)
             dx = ops.moe_gemm_dgrad_gate_up(dg, du, tiles, tg, tu, 1, dim) if ctx.needs_input_grad[0] else None
             offsets = torch.tensor([0, n_tokens], dtype=torch.int32, device=x.device)
             gg = ops.moe_gemm_wgrad(dg, x, offsets, 1)[0]

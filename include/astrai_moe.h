@@ -235,8 +235,10 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
  *             dx_perm = dg W_gate + du W_up,  dx = sum over slots (astrai_moe_combine)
  *             dW_down[e] = dy^T h,  dW_gate[e] = dg^T x_perm,  dW_up[e] = du^T x_perm
  *
- * astrai_moe_gemm_gate_up_train: astrai_moe_gemm_gate_up plus g and u
- *   ([n_rows, dim_ffn] bf16, the rounded projections silu and the product use).
+ * astrai_moe_gemm_gate_up_train: astrai_moe_gemm_gate_up plus gu
+ *   ([n_rows, 2 dim_ffn] bf16: the rounded projections silu and the product
+ *   use, interleaved per 4 columns: gu[r, 2c .. 2c+3] = g[r, c .. c+3] and
+ *   gu[r, 2c+4 .. 2c+7] = u[r, c .. c+3] for c a multiple of 4).
  * astrai_moe_gemm_down_train: astrai_moe_gemm_down plus y_unweighted
  *   ([n_rows, dim] bf16, the rounded expert output before the routing weight).
  */
@@ -245,7 +247,7 @@ int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles,
                                   const void* const* w_up, int dtype,
                                   int64_t n_rows, int n_experts, int64_t dim,
                                   int64_t dim_ffn, int block_m, void* h,
-                                  void* g, void* u, void* stream);
+                                  void* gu, void* stream);
 int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles,
                                int64_t tiles_len, const void* const* w_down,
                                const void* sorted_w, int dtype, int64_t n_rows,
@@ -269,11 +271,12 @@ int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token,
  *   dh = dy . W_down[e] (W_down [dim, dim_ffn]), rounded to bf16, then
  *   du = bf16(dh * silu(g)), dg = bf16(bf16(dh * u) * silu'(g))
  * (the order torch autograd takes through mlp.py:23).
- *   dy [n_rows, dim], g, u, dg, du [n_rows, dim_ffn], all bf16.
+ *   dy [n_rows, dim], gu [n_rows, 2 dim_ffn] (from astrai_moe_gemm_gate_up_train),
+ *   dg, du [n_rows, dim_ffn], all bf16.
  */
 int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles,
                                int64_t tiles_len, const void* const* w_down,
-                               const void* g, const void* u, int dtype,
+                               const void* gu, int dtype,
                                int64_t n_rows, int n_experts, int64_t dim,
                                int64_t dim_ffn, int block_m, void* dg, void* du,
                                void* stream);

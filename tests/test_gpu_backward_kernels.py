@@ -65,7 +65,8 @@ def test_backward_kernels(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew):
     perm, (wg, wu, wd), (tg, tu, td), gen = _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew)
     E = n_exp
     # training forward: h and y*w bit-identical to the inference kernels
-    h, g, u = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn)
+    h, gu = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn)
+    g, u = ops.gu_split(gu)
     y, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, E, dim)
     h_inf = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn, ops.TRAIN_BLOCK_M)
     y_inf = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, E, dim, ops.TRAIN_BLOCK_M)
@@ -76,7 +77,7 @@ def test_backward_kernels(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew):
     n_tokens = n_tok
     dout = torch.randn(n_tokens, dim, generator=gen, device=gpu).to(BF)
     dy, dw_rows = ops.moe_row_grad(dout, perm.sorted_token, perm.sorted_w, y_unw)
-    dg, du = ops.moe_gemm_dgrad_down(dy, perm.tiles, td, g, u, E)
+    dg, du = ops.moe_gemm_dgrad_down(dy, perm.tiles, td, gu, E)
     dx_perm = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim)
     dwd = ops.moe_gemm_wgrad(dy, h, perm.expert_offsets, E)
     dwg = ops.moe_gemm_wgrad(dg, perm.x_perm, perm.expert_offsets, E)
