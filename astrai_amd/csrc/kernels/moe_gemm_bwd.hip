@@ -87,6 +87,7 @@ struct BwdCfg {
   static_assert(BM * 64 * 2 == A_BYTES && BN * 64 * 2 == B_BYTES, "64-K stages");
   static_assert(LDS <= 160 * 1024, "LDS");
   static_assert(3 * OPS <= 63, "vmcnt range");
+  static_assert(16 % AR == 0 && 8 % RG == 0 && PD >= RG && PD + RG <= AR, "ring slots of a pair and its prefetch");
 };
 
 struct TileInfo {
@@ -302,9 +303,8 @@ __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][Bwd
   }
 }
 
-template <Bwd kMode>
-__global__ __launch_bounds__(BwdCfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs p) {
-  using Cfg = BwdCfg;
+template <Bwd kMode, typename Cfg = BwdCfg>
+__global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs p) {
   using Walk = std::conditional_t<kMode == Bwd::kWgrad, ExpertWalk, RowTileWalk>;
   constexpr bool kAMn = kMode == Bwd::kWgrad;  // A operand MN-major (B always is)
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
