@@ -31,6 +31,15 @@ int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
                      int64_t dim_ffn, int64_t dim, int block_m, bool packed,
                      void* y, hipStream_t s);
 
+// As launch_mfma_gate_up, reading the activation rows as x[sorted_token[r]]
+// (x: [n_tokens, dim]) instead of a copied x_perm.
+int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token,
+                               const int32_t* tiles, int64_t capacity,
+                               const void* const* w_gate,
+                               const void* const* w_up, int64_t dim,
+                               int64_t dim_ffn, int block_m, void* h,
+                               hipStream_t s);
+
 // Training forward (256-row tiles): as launch_mfma_gate_up / launch_mfma_down,
 // also storing the bf16 gate and up projections (gu: [rows, 2 dim_ffn],
 // blocks of 4 gate columns then the same 4 up columns) or the unweighted bf16

@@ -185,6 +185,28 @@ extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
                                      nullptr, dim, dim_ffn, h, s);
 }
 
+extern "C" int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token, int64_t n_tokens,
+                                              const int32_t* tiles, int64_t tiles_len, const void* const* w_gate,
+                                              const void* const* w_up, int dtype, int64_t n_rows, int n_experts,
+                                              int64_t dim, int64_t dim_ffn, int block_m, void* h, void* stream) {
+  clear_error();
+  int rc = check_common("gemm_gate_up_gather", x, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn, block_m,
+                        h);
+  if (rc) return rc;
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_gate_up_gather: bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(n_tokens >= 0 && n_tokens * dim * 2 < (1ll << 32),
+                 "gemm_gate_up_gather: x must be under 4 GiB (n_tokens %lld, dim %lld)", (long long)n_tokens,
+                 (long long)dim);
+  if (n_rows == 0) return ASTRAI_MOE_OK;
+  ASTRAI_REQUIRE(mfma_gate_up_supported(dim, dim_ffn, block_m, x, h),
+                 "gemm_gate_up_gather: unsupported shape (dim %lld, dim_ffn %lld, block_m %d) or alignment",
+                 (long long)dim, (long long)dim_ffn, block_m);
+  ASTRAI_REQUIRE(sorted_token && w_gate && w_up, "gemm_gate_up_gather: null row list or weight table");
+  const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  return launch_mfma_gate_up_gather(x, sorted_token, tiles, capacity, w_gate, w_up, dim, dim_ffn, block_m, h,
+                                    static_cast<hipStream_t>(stream));
+}
+
 extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                                     int64_t tiles_len,
                                     const void* const* w_down,

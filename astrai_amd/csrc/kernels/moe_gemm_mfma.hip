@@ -72,7 +72,9 @@ namespace {
 // weight rows of column tile nt are K / 64 contiguous blocks of BN x 128
 // bytes, each already in the staged (swizzled) LDS order, so a step's weight
 // load is one contiguous block.
-template <int BM, int BN, bool kGateUp, bool kPacked = false>
+// With kGather the activation rows are token rows of x read through the
+// permutation (GatherRows) rather than rows of a copied x_perm.
+template <int BM, int BN, bool kGateUp, bool kPacked = false, bool kGather = false>
 struct TileSrc {
   const char* a_base = nullptr;
   const char* b_base0 = nullptr;
@@ -84,7 +86,7 @@ struct TileSrc {
     const int e = ti[0];
     row0 = ti[1];
     rows = min(BM, ti[2] - row0);
-    a_base = reinterpret_cast<const char*>(A + (int64_t)row0 * K);
+    a_base = reinterpret_cast<const char*>(kGather ? A : A + (int64_t)row0 * K);
     if constexpr (kPacked) {
       b_base0 = static_cast<const char*>(W0[e]) + (int64_t)nt * (K / kBK) * (BN * kRowBytes);
       b_base1 = b_base0;
@@ -100,6 +102,10 @@ struct TileSrc {
     const uint32_t row = (uint32_t)min(q * 8 + dl.row, rows - 1);
     lds_dma_16(a_base + (row * k2 + dl.chunk(q)), lds);
   }
+  // 8-row group q of the A tile, the lane's row at byte offset row_off of x (gather)
+  __device__ void dma_a_rows(const DmaLane& dl, uint32_t row_off, int q, char* lds) const {
+    lds_dma_16(a_base + (row_off + dl.chunk(q)), lds);
+  }
   // 8-row group q of the B tile of K step kstep (up rows follow the gate rows)
   __device__ void dma_b(const DmaLane& dl, int lane, int kstep, int q, uint32_t k2, char* lds) const {
     if constexpr (kPacked) {
@@ -110,6 +116,22 @@ struct TileSrc {
       const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
       const int rq = (kGateUp && r0 >= BN / 2) ? r0 - BN / 2 : r0;
       lds_dma_16(bb + ((uint32_t)(rq + dl.row) * k2 + dl.chunk(q)), lds);
+    }
+  }
+};
+
+// Byte offsets in x of the token rows one lane loads in its NQ activation DMA
+// ops of a tile (ops qbase .. qbase + NQ - 1, row (q * 8 + lane / 8) of the
+// tile, pad rows re-reading the tile's last row), read from the permutation's
+// source-token list.
+template <int NQ>
+struct GatherRows {
+  uint32_t off[NQ];
+  __device__ void load(const int32_t* row_src, int row0, int rows, int qbase, int lane, uint32_t k2) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int r = min((qbase + i) * 8 + (lane >> 3), rows - 1);
+      off[i] = (uint32_t)row_src[row0 + r] * k2;
     }
   }
 };
@@ -290,11 +312,11 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
 
 // Position of a DMA wave in this workgroup's step sequence: the tile and K
 // step it loads next, and that tile's global bases.
-template <int BM, int BN, int GM, bool kGateUp, bool kPacked>
+template <int BM, int BN, int GM, bool kGateUp, bool kPacked, bool kGather = false>
 struct StepCursor {
   int logical, mt, nt, kt;
   bool live;
-  TileSrc<BM, BN, kGateUp, kPacked> src;
+  TileSrc<BM, BN, kGateUp, kPacked, kGather> src;
   __device__ void start(const TileWalk<GM>& walk, int logical_, int mt_, int nt_, const int32_t* tiles,
                         const bf16_t* A, const void* const* W0, const void* const* W1, int K) {
     logical = logical_, mt = mt_, nt = nt_, kt = 0, live = true;
@@ -312,11 +334,14 @@ struct StepCursor {
   }
 };
 
-template <bool kGateUp, bool kPacked, bool kSave>
+// kGather: A is x and the activation rows are gathered through row_src (the
+// permutation's source tokens).
+template <bool kGateUp, bool kPacked, bool kSave, bool kGather = false>
 __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
-    int capacity, bf16_t* __restrict__ C, bf16_t* __restrict__ S0, bf16_t* __restrict__ S1) {
+    int capacity, bf16_t* __restrict__ C, bf16_t* __restrict__ S0, bf16_t* __restrict__ S1,
+    const int32_t* __restrict__ row_src) {
   using Cfg = StreamCfg<kGateUp>;
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
 
@@ -340,18 +365,28 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     // ---------------- DMA waves ----------------
     const int dw = wave - Cfg::MW;
     const uint32_t k2 = (uint32_t)K * 2u;
-    StepCursor<Cfg::BM, Cfg::BN, Cfg::GM, kGateUp, kPacked> ca, cb;  // next A step, next B step
+    StepCursor<Cfg::BM, Cfg::BN, Cfg::GM, kGateUp, kPacked, kGather> ca;  // next A step
+    StepCursor<Cfg::BM, Cfg::BN, Cfg::GM, kGateUp, kPacked> cb;           // next B step
+    GatherRows<Cfg::OPS> grows;
+    auto load_rows = [&]() {
+      if constexpr (kGather) grows.load(row_src, ca.src.row0, ca.src.rows, dw * Cfg::OPS, lane, k2);
+    };
     ca.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
     cb.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
+    load_rows();
     auto issue_a = [&](int buf) {
       const DmaLane dl(lane, ca.kt);
       char* base = smem + Cfg::A_OFF + buf * Cfg::A_BYTES;
 #pragma unroll
       for (int i = 0; i < Cfg::OPS; ++i) {
         const int q = dw * Cfg::OPS + i;
-        ca.src.dma_a(dl, q, k2, base + q * 1024);
+        if constexpr (kGather)
+          ca.src.dma_a_rows(dl, grows.off[i], q, base + q * 1024);
+        else
+          ca.src.dma_a(dl, q, k2, base + q * 1024);
       }
       ca.advance(walk, tiles, A, W0, W1, K, KT);
+      if (ca.live && ca.kt == 0) load_rows();  // the next tile's rows
     };
     auto issue_b = [&](int buf) {
       const DmaLane dl(lane, cb.kt);
@@ -517,11 +552,11 @@ struct TileCfg {
   static_assert(DMA_PER_WAVE * (STAGES - 1) <= 63, "vmcnt range");
 };
 
-template <typename Cfg, bool kGateUp, bool kPacked>
+template <typename Cfg, bool kGateUp, bool kPacked, bool kGather = false>
 __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
-    int capacity, bf16_t* __restrict__ C) {
+    int capacity, bf16_t* __restrict__ C, const int32_t* __restrict__ row_src) {
   constexpr int S = Cfg::STAGES;
   constexpr int DPW = Cfg::DMA_PER_WAVE;
   constexpr int STAGE_AREA = S * Cfg::STAGE_BYTES;
@@ -541,7 +576,12 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   const uint32_t k2 = (uint32_t)K * 2u;
 
   static_assert(!kPacked || Cfg::BN == 256, "packed weights come in 256-row tiles");
-  TileSrc<Cfg::BM, Cfg::BN, kGateUp, kPacked> src;
+  TileSrc<Cfg::BM, Cfg::BN, kGateUp, kPacked, kGather> src;
+  GatherRows<Cfg::A_PER_WAVE> grows;
+  auto setup_tile = [&](int mt_, int nt_) {
+    src.setup(tiles, A, W0, W1, K, mt_, nt_);
+    if constexpr (kGather) grows.load(row_src, src.row0, src.rows, wave * Cfg::A_PER_WAVE, lane, k2);
+  };
   auto issue_stage = [&](int kstep, int buf) {
     char* sa = smem + buf * Cfg::STAGE_BYTES;
     char* sb = sa + Cfg::A_BYTES;
@@ -549,7 +589,10 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < Cfg::A_PER_WAVE; ++i) {
       const int q = wave * Cfg::A_PER_WAVE + i;
-      src.dma_a(dl, q, k2, sa + q * 1024);
+      if constexpr (kGather)
+        src.dma_a_rows(dl, grows.off[i], q, sa + q * 1024);
+      else
+        src.dma_a(dl, q, k2, sa + q * 1024);
     }
 #pragma unroll
     for (int i = 0; i < Cfg::B_PER_WAVE; ++i) {
@@ -607,7 +650,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   };
 
   const int KT = K / kBK;
-  src.setup(tiles, A, W0, W1, K, mt, nt);
+  setup_tile(mt, nt);
 #pragma unroll
   for (int s = 0; s < S; ++s)
     if (s < KT) issue_stage(s, s);
@@ -651,7 +694,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
     lds_barrier();  // every wave is done reading the stage buffers
     __builtin_amdgcn_sched_barrier(0);
     if (has_next) {
-      src.setup(tiles, A, W0, W1, K, nmt, nnt);
+      setup_tile(nmt, nnt);
 #pragma unroll
       for (int s = 0; s < S; ++s)
         if (s < KT) issue_stage(s, s);
@@ -671,32 +714,32 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
 using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8>;
 static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfmaBigBM, "prefill tile height");
 
-template <bool kGateUp, bool kPacked, bool kSave = false>
+template <bool kGateUp, bool kPacked, bool kSave = false, bool kGather = false>
 int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
                   const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s, void* S0 = nullptr,
-                  void* S1 = nullptr) {
+                  void* S1 = nullptr, const int32_t* row_src = nullptr) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   using Cfg = StreamCfg<kGateUp>;
   const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked, kSave>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
-                     static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
-                     (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0),
-                     static_cast<bf16_t*>(S1));
+  hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked, kSave, kGather>), dim3((unsigned)grid),
+                     dim3(Cfg::THREADS), 0, s, static_cast<const bf16_t*>(A), tiles, W0, W1,
+                     static_cast<const bf16_t*>(row_w), (int)K, (int)N, (int)n_tiles_n, (int)capacity,
+                     static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0), static_cast<bf16_t*>(S1), row_src);
   return check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>");
 }
 
-template <typename Cfg, bool kGateUp, bool kPacked>
+template <typename Cfg, bool kGateUp, bool kPacked, bool kGather = false>
 int launch(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
-           const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s) {
+           const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s, const int32_t* row_src = nullptr) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  hipLaunchKernelGGL((gemm_mfma_kernel<Cfg, kGateUp, kPacked>), dim3((unsigned)grid), dim3(Cfg::THREADS), 0, s,
-                     static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K, (int)N,
-                     (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C));
+  hipLaunchKernelGGL((gemm_mfma_kernel<Cfg, kGateUp, kPacked, kGather>), dim3((unsigned)grid), dim3(Cfg::THREADS),
+                     0, s, static_cast<const bf16_t*>(A), tiles, W0, W1, static_cast<const bf16_t*>(row_w), (int)K,
+                     (int)N, (int)n_tiles_n, (int)capacity, static_cast<bf16_t*>(C), row_src);
   return check_launch(kGateUp ? "gemm_mfma_kernel<gate_up>" : "gemm_mfma_kernel<down>");
 }
 
@@ -755,6 +798,16 @@ int launch_mfma_down_save(const void* h, const int32_t* tiles, int64_t capacity,
                           hipStream_t s) {
   return launch_stream<false, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
                                            y_unweighted, nullptr);
+}
+
+int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token, const int32_t* tiles, int64_t capacity,
+                               const void* const* w_gate, const void* const* w_up, int64_t dim, int64_t dim_ffn,
+                               int block_m, void* h, hipStream_t s) {
+  if (block_m == kMfmaBigBM)
+    return launch_stream<true, false, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
+                                                   nullptr, nullptr, sorted_token);
+  return launch<SmallCfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
+                                             sorted_token);
 }
 
 int launch_pack(const void* w0, const void* w1, int64_t rows, int64_t k, bool gate_up, void* out, hipStream_t s) {

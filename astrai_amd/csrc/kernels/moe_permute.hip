@@ -187,6 +187,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     }
   }
   __syncthreads();
+  if (x_perm == nullptr) return;  // index outputs only (the GEMM gathers the rows itself)
 
   // Row copy: each token row is read once and written top_k times.
   const int wave = threadIdx.x >> 6;
@@ -241,7 +242,7 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
   const int64_t nunits = vec ? dim * (int64_t)sizeof(T) / 16 : dim;
   int64_t splits = ceil_div(512, nc);
   if (splits > nunits / 64) splits = nunits / 64;
-  if (splits < 1) splits = 1;
+  if (splits < 1 || x_perm == nullptr) splits = 1;
   if (splits > 65535) splits = 65535;
   const dim3 grid((unsigned)nc, (unsigned)splits);
   if (vec)
@@ -297,9 +298,9 @@ extern "C" int astrai_moe_permute(
   ASTRAI_REQUIRE(tiles_len >= need,
                  "permute: tile list holds %lld int32, needs %lld",
                  (long long)tiles_len, (long long)need);
-  ASTRAI_REQUIRE(topk_idx && topk_w && chunk_hist && x && expert_offsets &&
-                     sorted_token && sorted_w && token_pos && x_perm && tiles &&
-                     chunk_base,
+  ASTRAI_REQUIRE(topk_idx && topk_w && chunk_hist && (x || !x_perm) &&
+                     expert_offsets && sorted_token && sorted_w && token_pos &&
+                     tiles && chunk_base,
                  "permute: null buffer");
   const int64_t capacity =
       (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;

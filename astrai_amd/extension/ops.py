@@ -48,7 +48,7 @@ class PermuteResult(NamedTuple):
     sorted_token: torch.Tensor  # [T*K] int32
     sorted_w: torch.Tensor  # [T*K] dtype
     token_pos: torch.Tensor  # [T, K] int32
-    x_perm: torch.Tensor  # [T*K, D] dtype
+    x_perm: torch.Tensor | None  # [T*K, D] dtype (None: rows not copied)
     tiles: torch.Tensor  # tile list, int32
     block_m: int
 
@@ -147,9 +147,12 @@ def moe_route(logits: torch.Tensor, top_k: int) -> RouteResult:
     return RouteResult(topk_idx, topk_w, chunk_hist)
 
 
-def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: int) -> PermuteResult:
+def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: int,
+                copy_rows: bool = True) -> PermuteResult:
     """Expert-major, token-ascending permutation of the routed rows
-    (mlp.py:90-95) plus the device-built GEMM tile list."""
+    (mlp.py:90-95) plus the device-built GEMM tile list. ``copy_rows=False``
+    writes the index outputs only (``x_perm`` is None), for
+    ``moe_gemm_gate_up_gather``."""
     fn = _kernel("moe_permute")
     _require_gpu(x, "x", 2)
     code = _dtype_code(x, "x")
@@ -167,13 +170,13 @@ def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: in
     sorted_token = torch.empty(rows, dtype=torch.int32, device=dev)
     sorted_w = torch.empty(rows, dtype=x.dtype, device=dev)
     token_pos = torch.empty(n_tokens, top_k, dtype=torch.int32, device=dev)
-    x_perm = torch.empty(rows, dim, dtype=x.dtype, device=dev)
+    x_perm = torch.empty(rows, dim, dtype=x.dtype, device=dev) if copy_rows else None
     tiles = torch.empty(tl, dtype=torch.int32, device=dev)
     chunk_base = torch.empty_like(chunk_hist)
     _check(
         fn(topk_idx.data_ptr(), topk_w.data_ptr(), chunk_hist.data_ptr(), x.data_ptr(), code, n_tokens, n_experts,
            top_k, dim, block_m, offsets.data_ptr(), sorted_token.data_ptr(), sorted_w.data_ptr(),
-           token_pos.data_ptr(), x_perm.data_ptr(), tiles.data_ptr(), tl, chunk_base.data_ptr(), _stream(x)),
+           token_pos.data_ptr(), _ptr(x_perm), tiles.data_ptr(), tl, chunk_base.data_ptr(), _stream(x)),
         "moe_permute",
     )
     return PermuteResult(offsets, sorted_token, sorted_w, token_pos, x_perm, tiles, block_m)
@@ -213,6 +216,30 @@ def _out_buffer(out: torch.Tensor | None, rows: int, cols: int, like: torch.Tens
     if tuple(out.shape) != (rows, cols) or out.dtype != like.dtype or out.device != like.device:
         raise ValueError(f"out must be [{rows}, {cols}] {like.dtype} on {like.device}")
     return out
+
+
+def gather_supported(n_tokens: int, dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
+    """Whether ``moe_gemm_gate_up_gather`` takes this problem (bf16, the
+    matrix-core shapes, x under 4 GiB)."""
+    return packed_supported(dim, dim_ffn, dtype) and n_tokens * dim * 2 < 1 << 32
+
+
+def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor,
+                            w_up: torch.Tensor, n_experts: int, dim_ffn: int, block_m: int) -> torch.Tensor:
+    """``moe_gemm_gate_up`` on the permuted rows ``x[sorted_token]`` read
+    straight from ``x`` (no copied ``x_perm``); bit-identical results."""
+    _require_gpu(x, "x", 2)
+    code = _dtype_code(x, "x")
+    n_tokens, dim = x.shape
+    n_rows = sorted_token.numel()
+    h = torch.empty(n_rows, dim_ffn, dtype=x.dtype, device=x.device)
+    _check(
+        loader.library().astrai_moe_gemm_gate_up_gather(
+            x.data_ptr(), sorted_token.data_ptr(), n_tokens, tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
+            w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, block_m, h.data_ptr(), _stream(x)),
+        "moe_gemm_gate_up_gather",
+    )
+    return h
 
 
 def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
@@ -346,8 +373,13 @@ def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tens
         return torch.empty(0, dim, dtype=x.dtype, device=x.device)
     block_m = select_block_m(n_tokens, n_experts, top_k, dim, dim_ffn, x.dtype)
     route = moe_route(logits, top_k)
-    perm = moe_permute(route, x, n_experts, block_m)
-    h = moe_gemm_gate_up(perm.x_perm, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m, packed=packed)
+    if not packed and gather_supported(n_tokens, dim, dim_ffn, x.dtype):
+        # the gate/up GEMM reads the token rows itself: no copied x_perm
+        perm = moe_permute(route, x, n_experts, block_m, copy_rows=False)
+        h = moe_gemm_gate_up_gather(x, perm.sorted_token, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m)
+    else:
+        perm = moe_permute(route, x, n_experts, block_m)
+        h = moe_gemm_gate_up(perm.x_perm, perm.tiles, w_gate, w_up, n_experts, dim_ffn, block_m, packed=packed)
     y = moe_gemm_down(h, perm.tiles, w_down, perm.sorted_w, n_experts, dim, block_m, packed=packed)
     return moe_combine(y, perm.token_pos, shared)
 

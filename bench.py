@@ -67,7 +67,10 @@ class StageTimer:
     """Wraps the ops entry points to record HIP events around each launch on
     the current stream (the stream the kernels are enqueued on)."""
 
-    STAGES = ("moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_down", "moe_combine")
+    STAGES = ("moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_gate_up_gather", "moe_gemm_down",
+              "moe_combine")
+    # the gate/up GEMM reading x through the permutation counts as the gate/up stage
+    MERGE = {"moe_gemm_gate_up_gather": "moe_gemm_gate_up"}
 
     def __init__(self, ops):
         self.ops = ops
@@ -95,7 +98,10 @@ class StageTimer:
             setattr(self.ops, name, fn)
 
     def avg_ms(self) -> dict[str, float]:
-        return {k: (sum(s.elapsed_time(e) for s, e in v) / len(v) if v else 0.0) for k, v in self.events.items()}
+        events: dict[str, list] = {}
+        for k, v in self.events.items():
+            events.setdefault(self.MERGE.get(k, k), []).extend(v)
+        return {k: (sum(s.elapsed_time(e) for s, e in v) / len(v) if v else 0.0) for k, v in events.items()}
 
 
 def cpu_baseline(layer, x, w, target_s: float) -> dict:
@@ -232,6 +238,7 @@ def main():
         layer.requires_grad_(False)
 
     bf16 = w.dtype == torch.bfloat16
+    gathered = not layer.uses_packed_weights(w.dtype) and ops.gather_supported(T, w.dim, w.dim_ffn, w.dtype)
     s = 2 if bf16 else 4
     peak = PEAK_BF16_TFLOPS if bf16 else PEAK_FP32_TFLOPS
     rows = T * w.top_k
@@ -278,7 +285,9 @@ def main():
         "gemm_frac_of_peak": gemm_tflops / peak,
         "roofline": roofline,
         "kernels_ms": stage_ms,
-        "permute_gbs": bytes_permute / (stage_ms["moe_permute"] / 1e3) / 1e9,
+        # with the gathering gate/up GEMM the permutation writes indices only (its rows are read by the GEMM)
+        "permute_gbs": (bytes_permute / (stage_ms["moe_permute"] / 1e3) / 1e9) if not gathered else None,
+        "permute_rows": "gathered by the gate/up GEMM (no x_perm copy)" if gathered else "copied to x_perm",
         "combine_gbs": bytes_combine / (stage_ms["moe_combine"] / 1e3) / 1e9,
         "expert_weight_stream_gbs": weight_bytes / (t_gu + t_dn) / 1e9,
         "routing": routing_stats(counts),

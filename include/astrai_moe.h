@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 3
+#define ASTRAI_MOE_ABI_VERSION 4
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -108,7 +108,10 @@ int astrai_moe_route(const void* logits, int dtype, int64_t n_tokens,
  *   sorted_token   [n_tokens * top_k]    int32, source token of each row
  *   sorted_w       [n_tokens * top_k]    dtype, routing weight of each row
  *   token_pos      [n_tokens * top_k]    int32, row of (token, slot)
- *   x_perm         [n_tokens * top_k, dim] dtype, x[sorted_token]
+ *   x_perm         [n_tokens * top_k, dim] dtype, x[sorted_token]; may be NULL:
+ *                  then only the index outputs are written (and x may be NULL
+ *                  too), for astrai_moe_gemm_gate_up_gather, which reads the
+ *                  token rows of x itself
  *   tiles          astrai_moe_tile_list_len(...) int32, see layout above
  *   chunk_base     [n_chunks, n_experts] int32 scratch
  */
@@ -136,6 +139,24 @@ int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
                             const void* const* w_up, int dtype, int64_t n_rows,
                             int n_experts, int64_t dim, int64_t dim_ffn,
                             int block_m, void* h, void* stream);
+
+/*
+ * astrai_moe_gemm_gate_up reading the activation rows straight from x: row r
+ * of the permuted input is x[sorted_token[r]], so the permutation need not
+ * copy x (astrai_moe_permute with x_perm = NULL). Same results as
+ * astrai_moe_gemm_gate_up on the copied rows (bit-identical). bf16 and the
+ * matrix-core block sizes (32 or 256) only; x under 4 GiB.
+ *
+ *   x             [n_tokens, dim]   bf16
+ *   sorted_token  [n_rows]          int32, from astrai_moe_permute
+ */
+int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token,
+                                   int64_t n_tokens, const int32_t* tiles,
+                                   int64_t tiles_len, const void* const* w_gate,
+                                   const void* const* w_up, int dtype,
+                                   int64_t n_rows, int n_experts, int64_t dim,
+                                   int64_t dim_ffn, int block_m, void* h,
+                                   void* stream);
 
 /*
  * Grouped down projection with the routing-weight multiply fused.

@@ -175,6 +175,39 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
         torch.testing.assert_close(y[a:b], y_ref, **tol)
 
 
+@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
+    (2048, 8, 2, 1024, 1536),  # 256-row tiles
+    (300, 16, 4, 512, 256),  # 32-row tiles
+    (64, 128, 8, 4096, 1536),  # decode-sized loads, some experts empty
+    (16384, 4, 2, 256, 128),  # many rows per expert, several tiles per workgroup
+    (1, 8, 2, 256, 128),  # one token
+])
+def test_gate_up_gather_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
+    # the gate/up GEMM reading x[sorted_token] directly equals the GEMM on the
+    # copied x_perm, and the index-only permutation equals the full one
+    dtype = torch.bfloat16
+    assert ops.gather_supported(n_tok, dim, dim_ffn, dtype)
+    route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=12)
+    g = torch.Generator(device=gpu).manual_seed(13)
+    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=14)
+    bm = ops.select_block_m(n_tok, n_exp, top_k, dim, dim_ffn, dtype)
+    assert bm in (32, 256)
+    perm = ops.moe_permute(route, x, n_exp, bm)
+    idx = ops.moe_permute(route, x, n_exp, bm, copy_rows=False)
+    assert idx.x_perm is None
+    for a, b in zip(perm[:4], idx[:4]):
+        assert torch.equal(a, b)
+    n_live = perm.tiles[0].item()  # entries past the live tiles are never written
+    assert torch.equal(perm.tiles[:4 + 3 * n_live], idx.tiles[:4 + 3 * n_live])
+    tg = ops.expert_weight_table([e.gate for e in experts], (dim_ffn, dim))
+    tu = ops.expert_weight_table([e.up for e in experts], (dim_ffn, dim))
+    h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    hg = ops.moe_gemm_gate_up_gather(x, idx.sorted_token, idx.tiles, tg, tu, n_exp, dim_ffn, bm)
+    torch.cuda.synchronize()
+    assert torch.equal(hg, h)
+
+
 def _packed_layout(w0, w1, tile_rows):
     """Expected packed order of one expert's weight: per column tile of 256
     rows (gate/up: ``tile_rows`` = 128 gate rows then the same 128 up rows;
