@@ -39,7 +39,7 @@ PEAK_HBM_GBS = 8000.0
 # (it counts this part's 128-byte read requests as 64 bytes). Source:
 # profiles/moe_layer_d4096_f14336_e8_k2_t16384.md.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
-    "moe_bf16_d4096_f14336_e8_k2_t16384": (6429325.9 * 2 + 917520.3) * 1024,
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (6483612.4 * 2 + 917551.1) * 1024,
 }
 
 
@@ -257,11 +257,12 @@ def main():
         # decode-sized loads: the gate/up kernel streams the routed experts' weights
         gu_bytes = n_active * 2.0 * w.dim * w.dim_ffn * s + rows * w.dim * s + rows * w.dim_ffn * s
         gbs = gu_bytes / t_gu / 1e9
-        roofline = {"kernel": "gemm_mfma_kernel<gate_up>", "bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
+        roofline = {"kernel": "gemm_mfma_kernel<gate_up" + (", gather>" if gathered else ">"), "bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": traffic,
                     "algorithmic_bytes_per_launch": gu_bytes}
     else:
-        roofline = {"kernel": ("gemm_stream_kernel<gate_up>" if bf16 else "gemm_generic_kernel<gate_up>"),
+        roofline = {"kernel": (("gemm_stream_kernel<gate_up, gather>" if gathered else "gemm_stream_kernel<gate_up>")
+                               if bf16 else "gemm_generic_kernel<gate_up>"),
                     "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
                     "traffic": traffic, "algorithmic_flops_per_launch": flops_gate_up}
 
