@@ -31,26 +31,36 @@
 //   128 x 64 each; waves 8-11 (one per SIMD) only issue the LDS DMA. An LDS-DMA
 //   op holds its wave until the CU's vector memory path accepts it (about 1 KB
 //   per 15 cycles), so in the earlier design, where matrix-core waves issued
-//   the DMA themselves, that wait came out of their MFMA schedule. Two 64 KB
-//   stages; one s_barrier per 64-K step, placed where every matrix-core wave
-//   has finished reading the step's buffer: after it the DMA waves refill that
-//   buffer with step g + 2 (expert weights first: they come from HBM and land
-//   last) and the matrix-core waves read step g + 1, whose data the DMA waves
-//   waited for before the barrier. The matrix-core waves stream A fragments
-//   through a ring of four registers two rows ahead and reload each B fragment
-//   in place right after its last use, which keeps them at 166 VGPRs (the
-//   register file holds three waves of 168 per SIMD) with no spills.
+//   the DMA themselves, that wait came out of their MFMA schedule. LDS holds
+//   two 32 KB activation stages and three 32 KB weight stages (160 KB); one
+//   s_barrier per 64-K step, placed where every matrix-core wave has finished
+//   reading the step's buffers: after it the DMA waves load the activations of
+//   step g + 2 and the weights of step g + 3 (they come from HBM and get two
+//   steps to land) and the matrix-core waves read step g + 1, whose data the
+//   DMA waves waited for before the barrier. The matrix-core waves stream A
+//   fragments through a ring of four registers two rows ahead and reload each
+//   B fragment in place right after its last use, which keeps them within 168
+//   VGPRs (the register file holds three waves of 168 per SIMD) with no
+//   spills; every step, a tile's last included, prefetches the next step's
+//   first fragments, so the K loop is one body with one register assignment.
+//   The epilogue stores 8-byte row pieces straight from the accumulators.
 //
 // * gemm_mfma_kernel (32-row tiles, decode): 4 waves of 32 x 64, every wave
-//   issues DMA, four 32 KB stages in flight to keep the expert-weight stream
-//   busy; MFMA fragments are double-buffered per 32-K half.
+//   issues DMA, four 36 KB stages in flight to keep the expert-weight stream
+//   busy; MFMA fragments are double-buffered per 32-K half; the epilogue
+//   stages 16-row pieces per wave in LDS and stores 16-byte row segments.
+//
+// Variants (template flags): kPacked reads the weights from a packed copy
+// (pack_kernel: one contiguous 32 KB block per 256-row tile and 64-K step);
+// kSave (training forward) also stores what the backward needs; kGather
+// (gate/up) reads the activation rows as x[sorted_token[r]] instead of from a
+// copied x_perm.
 //
 // Epilogue: accumulators are rounded to bf16 with the hardware converter
 // (v_cvt_pk_bf16_f32, round-to-nearest-even), SiLU is g * rcp(1 + 2^(-g*log2e))
 // on v_exp_f32 / v_rcp_f32 (within 2 ulp of the libm form before its bf16
 // rounding). The weight fragment is the MFMA's first operand, which leaves
-// each lane 4 consecutive output columns of one row; each wave stages
-// 16-row pieces in LDS with 8-byte writes and stores 16-byte row segments.
+// each lane 4 consecutive output columns of one row.
 //
 // Scheduling: one persistent workgroup per CU walks the tile list. Workgroup
 // ids are dealt round-robin to the 8 XCDs, so each XCD's workgroups take a
