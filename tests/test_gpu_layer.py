@@ -177,3 +177,34 @@ def test_packed_weights_match_live_weights_and_follow_updates(gpu, tmp_path):
         out3 = both(a)
         assert not torch.equal(out3, b(x))
         check_layer(a, x, "packed after swapped up weights")
+
+
+def _random_configs(n, seed):
+    import random
+
+    rnd = random.Random(seed)
+    out = []
+    for _ in range(n):
+        dtype = torch.bfloat16 if rnd.random() < 0.8 else torch.float32
+        if rnd.random() < 0.6:  # shapes the matrix-core kernels take
+            dim, dim_ffn = 256 * rnd.randint(1, 4), 128 * rnd.randint(1, 6)
+        else:
+            dim, dim_ffn = 8 * rnd.randint(1, 40), 8 * rnd.randint(1, 40)
+        n_exp = rnd.choice([1, 2, 3, 8, 16, 33, 64])
+        top_k = rnd.randint(1, min(n_exp, 8))
+        n_shared = rnd.choice([0, 0, 1, 2])
+        n_tok = rnd.choice([1, 5, 31, 64, 257, 700, 1500])
+        out.append((dim, dim_ffn, n_exp, n_shared, top_k, dtype, n_tok, rnd.random() < 0.3))
+    return out
+
+
+@pytest.mark.parametrize("dim,dim_ffn,n_exp,n_shared,top_k,dtype,n_tok,pack", _random_configs(24, seed=2024))
+def test_random_shapes(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, n_tok, pack):
+    # seeded random shapes across both kernel families, decode- and prefill-sized
+    # row counts, shared experts, E = 1 and top_k = E, with and without the
+    # packed weight copy (which only bf16 matrix-core shapes use)
+    layer = _random_layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, seed=n_tok + dim)
+    layer.pack_weights = pack
+    g = torch.Generator(device=gpu).manual_seed(dim * 7 + n_tok)
+    x = torch.randn(1, n_tok, dim, generator=g, device=gpu).to(dtype)
+    check_layer(layer, x, f"d{dim}_f{dim_ffn}_e{n_exp}_s{n_shared}_k{top_k}_{dtype}_t{n_tok}_p{int(pack)}")
