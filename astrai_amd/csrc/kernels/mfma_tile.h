@@ -63,29 +63,34 @@ __device__ inline void lds_barrier() {
 
 // The persistent tile walk. Round r takes logical tile r * G + slot, where
 // slot gives the workgroups of one XCD a contiguous range of logical tiles;
-// logical tiles walk GM row tiles for every column tile. Dead row tiles (past
-// the live count the tile list reports) are skipped.
+// logical tiles walk GM row tiles for every column tile.
 template <int GM>
 struct TileWalk {
-  int G, total, n_live, group_size, capacity;
-  __device__ TileWalk(const int32_t* tiles, int capacity_, int n_tiles_n)
-      : G((int)gridDim.x), total(capacity_ * n_tiles_n), n_live(min(tiles[0], tiles[2])),
-        group_size(GM * n_tiles_n), capacity(capacity_) {}
+  int G, n_live, total, group_size;
+  // Only the live row tiles (tiles[0] of them) enter the logical order, and
+  // the last group holds just the live tiles left, so the live logical tiles
+  // are exactly [0, total) and each round but the last is full. (Sizing the
+  // last group by the list's capacity instead spread its live tiles over
+  // several mostly empty rounds.)
+  __device__ TileWalk(const int32_t* tiles, int capacity, int n_tiles_n)
+      : G((int)gridDim.x),
+        n_live(min(tiles[0], min(tiles[2], capacity))),
+        total(n_live * n_tiles_n),
+        group_size(GM * n_tiles_n) {}
   __device__ int first_slot() const {
     const int bid = blockIdx.x;
     return (G % kXcds == 0) ? (bid % kXcds) * (G / kXcds) + bid / kXcds : bid;
   }
-  __device__ bool decode(int logical, int& mt, int& nt) const {
+  __device__ void decode(int logical, int& mt, int& nt) const {
     const int first_m = (logical / group_size) * GM;
-    const int gm = min(GM, capacity - first_m);
+    const int gm = min(GM, n_live - first_m);
     const int in_group = logical - (first_m / GM) * group_size;
     mt = first_m + in_group % gm;
     nt = in_group / gm;
-    return mt < n_live;
   }
-  // the first live logical tile at or after `logical` in this workgroup's sequence (>= total: none)
+  // this workgroup's tile at `logical` (>= total: none)
   __device__ int seek(int logical, int& mt, int& nt) const {
-    while (logical < total && !decode(logical, mt, nt)) logical += G;
+    if (logical < total) decode(logical, mt, nt);
     return logical;
   }
 };
