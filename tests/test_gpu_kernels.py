@@ -261,6 +261,52 @@ def test_packed_gemms_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     assert torch.equal(yp, y)
 
 
+@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
+    (64, 128, 8, 4096, 1536),  # decode shape: <= 10 rows per expert, some experts empty
+    (64, 8, 2, 4096, 2048),  # few experts, many column tiles per expert
+    (2048, 8, 2, 1024, 1280),  # many row tiles per expert, several tiles per workgroup
+    (700, 16, 4, 2048, 768),  # ragged row tiles
+    (1, 8, 2, 1024, 1024),  # one token
+])
+def test_decode_gemms_row_strided_packed_gathered_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
+    # 32-row tiles: row-strided, packed and gathered operands give equal bits,
+    # and every expert's rows match torch
+    dtype, bm = torch.bfloat16, 32
+    route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=21)
+    g = torch.Generator(device=gpu).manual_seed(22)
+    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=23)
+    perm = ops.moe_permute(route, x, n_exp, bm)
+    tg = ops.expert_weight_table([e.gate for e in experts], (dim_ffn, dim))
+    tu = ops.expert_weight_table([e.up for e in experts], (dim_ffn, dim))
+    td = ops.expert_weight_table([e.down for e in experts], (dim, dim_ffn))
+    h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    hg = ops.moe_gemm_gate_up_gather(x, perm.sorted_token, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm)
+    pg = [ops.moe_pack_gate_up(e.gate, e.up) for e in experts]  # the tables hold pointers: keep the copies
+    pd = [ops.moe_pack_down(e.down) for e in experts]
+    tpg = ops.expert_weight_table(pg, (2 * dim_ffn, dim))
+    tpd = ops.expert_weight_table(pd, (dim, dim_ffn))
+    hp = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tpg, tpg, n_exp, dim_ffn, bm, packed=True)
+    yp = ops.moe_gemm_down(h, perm.tiles, tpd, perm.sorted_w, n_exp, dim, bm, packed=True)
+    torch.cuda.synchronize()
+    assert torch.equal(h, hp)
+    assert torch.equal(hg, hp)
+    assert torch.equal(y, yp)
+    # and against torch, per expert (first rows of the output only where rows exist)
+    offs = perm.expert_offsets.tolist()
+    for e in range(n_exp):
+        a, b = offs[e], offs[e + 1]
+        if a == b:
+            continue
+        w = experts[e]
+        xe = perm.x_perm[a:b]
+        h_ref = F.linear(xe, w.up) * F.silu(F.linear(xe, w.gate))  # mlp.py:23
+        torch.testing.assert_close(h[a:b], h_ref, **BF16_TOL)
+        y_ref = F.linear(h[a:b], w.down) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
+        torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
+
+
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,n_shared,dtype", [
     (1000, 8, 2, 256, 0, torch.bfloat16),
     (513, 16, 5, 128, 0, torch.bfloat16),
