@@ -227,6 +227,38 @@ def _packed_layout(w0, w1, tile_rows):
     return blocks.gather(3, idx).reshape(-1, k)
 
 
+@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn,block_m", [
+    (600, 2, 2, 1024, 65536, 256),  # down K = 65536: 128 KB weight rows, 32 MB per 256-row tile
+    (300, 2, 1, 65536, 256, 256),  # gate/up K = 65536
+    (64, 2, 2, 65536, 512, 32),  # the 32-row kernels at the same K
+])
+def test_long_k_rows(gpu, n_tok, n_exp, top_k, dim, dim_ffn, block_m):
+    # byte offsets within a tile grow with K (rows x K x 2 bytes, 32-bit in the
+    # kernels): long rows against torch, per expert
+    dtype = torch.bfloat16
+    route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=31)
+    g = torch.Generator(device=gpu).manual_seed(32)
+    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=33)
+    perm = ops.moe_permute(route, x, n_exp, block_m)
+    tg = ops.expert_weight_table([e.gate for e in experts], (dim_ffn, dim))
+    tu = ops.expert_weight_table([e.up for e in experts], (dim_ffn, dim))
+    td = ops.expert_weight_table([e.down for e in experts], (dim, dim_ffn))
+    h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, block_m)
+    y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, block_m)
+    torch.cuda.synchronize()
+    offs = perm.expert_offsets.tolist()
+    for e, w in enumerate(experts):
+        a, b = offs[e], offs[e + 1]
+        if a == b:
+            continue
+        xe = perm.x_perm[a:b]
+        h_ref = F.linear(xe, w.up) * F.silu(F.linear(xe, w.gate))  # mlp.py:23
+        torch.testing.assert_close(h[a:b], h_ref, **BF16_TOL)
+        y_ref = F.linear(h[a:b], w.down) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
+        torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
+
+
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
     (2048, 8, 2, 1024, 1536),  # 256-row tiles
     (300, 16, 4, 512, 256),  # 32-row tiles
