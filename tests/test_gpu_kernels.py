@@ -62,6 +62,8 @@ ROUTE_CASES = [
     (64, 5, 5, torch.bfloat16, 1.0),
     (256, 1, 1, torch.bfloat16, 1.0),
     (1024, 16, 1, torch.float32, 0.3),
+    (262144, 64, 6, torch.bfloat16, 0.9),  # many chunks of the device-side histogram
+    (100003, 32, 4, torch.float32, 1.0),  # ragged last chunk
 ]
 
 
@@ -92,6 +94,8 @@ PERM_CASES = [
     (2048, 128, 8, 512, 32),
     (1000, 3, 2, 40, 64),
     (500, 1024, 4, 64, 32),
+    (262144, 64, 6, 64, 256),  # 1.57 M rows, many chunks in the scan
+    (100003, 32, 4, 72, 32),  # ragged last chunk; rows copied element-wise (72 x 2 bytes is not 16-byte aligned)
 ]
 
 
