@@ -43,7 +43,8 @@
 //   VGPRs (the register file holds three waves of 168 per SIMD) with no
 //   spills; every step, a tile's last included, prefetches the next step's
 //   first fragments, so the K loop is one body with one register assignment.
-//   The epilogue stores 8-byte row pieces straight from the accumulators.
+//   The epilogue stores straight from the accumulators, after a lane-group
+//   transpose (v_permlane32/16_swap) that gives each lane 16-byte row pieces.
 //
 // * gemm_mfma_kernel (32-row tiles, decode): 4 waves of 32 x 64, every wave
 //   issues DMA, four 36 KB stages in flight to keep the expert-weight stream
@@ -259,61 +260,105 @@ struct StreamCfg {
   static_assert(3 * OPS <= 63, "vmcnt range");
 };
 
-// Epilogue straight from the accumulators: lane l holds 4 consecutive output
-// columns of one row per 16x16 tile, stored as one 8-byte write (rows of a
-// tile are written by 16 lanes at once; L2 merges the pieces of each line).
-// kSave (training forward) also stores what the backward needs: for gate/up
-// the bf16 gate and up projections interleaved in blocks of 4 columns (S0
-// [rows, 2 N]: g[c..c+3] then u[c..c+3] at 2 c, one 16-byte store per lane,
-// so each wave completes whole 128-byte lines), for down the unweighted bf16
-// expert output (S0, at C's positions).
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// Cross-lane exchanges of gfx950 on 8-byte values (one per lane): swap32
+// trades lanes 32-63 of a for lanes 0-31 of b, swap16 trades the odd 16-lane
+// rows of a (lanes 16-31, 48-63) for the even rows of b. Lane l keeps its
+// l % 16 either way.
+__device__ __forceinline__ void swap32(bf16x4_t& a, bf16x4_t& b) {
+  const u32x2_t x = __builtin_bit_cast(u32x2_t, a), y = __builtin_bit_cast(u32x2_t, b);
+  const auto r0 = __builtin_amdgcn_permlane32_swap(x[0], y[0], false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap(x[1], y[1], false, false);
+  a = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[0], r1[0]});
+  b = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[1], r1[1]});
+}
+__device__ __forceinline__ void swap16(bf16x4_t& a, bf16x4_t& b) {
+  const u32x2_t x = __builtin_bit_cast(u32x2_t, a), y = __builtin_bit_cast(u32x2_t, b);
+  const auto r0 = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+  const auto r1 = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+  a = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[0], r1[0]});
+  b = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[1], r1[1]});
+}
+// e[j] of lane (row r, group q = l / 16) holds columns 16 j + 4 q .. +3 of row
+// r (two 16-column tiles). Afterwards lane q holds columns 8 q .. 8 q + 7 of
+// the 32 (e[0] then e[1]): one 16-byte store, and the 4 lanes of a row cover
+// its 64 bytes contiguously.
+__device__ __forceinline__ void transpose2(bf16x4_t (&e)[2]) {
+  swap32(e[0], e[1]);
+  swap16(e[0], e[1]);
+}
+
+// Epilogue straight from the accumulators. Lane l holds 4 consecutive output
+// columns of one row per 16x16 tile; a lane-group transpose (above) per pair
+// of tiles first gathers each lane 8 consecutive columns, so a row block of 16
+// rows goes out in 16-byte stores, each instruction covering 64 contiguous
+// bytes of each of its 16 rows (half the store instructions and cache-line
+// requests of 8-byte pieces; the stores share the load path with the next
+// tile's DMA). kSave (training forward) also stores what the backward needs:
+// for gate/up the bf16 gate and up projections interleaved in blocks of 4
+// columns (S0 [rows, 2 N]: g[c..c+3] then u[c..c+3] at 2 c, one 16-byte store
+// per lane, so each wave completes whole 128-byte lines), for down the
+// unweighted bf16 expert output (S0, at C's positions).
 template <bool kGateUp, int WM, int WN, int BN, bool kSave>
 __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 16], const bf16_t* row_w, bf16_t* C,
                                                   int N, int wm, int wn, int t_row0, int t_rows, int t_nt,
                                                   bf16_t* S0, bf16_t* S1) {
   constexpr int MT16 = WM / 16, NT16 = WN / 16;
+  constexpr int NJ = kGateUp ? NT16 / 2 : NT16;  // output tiles of 16 columns
+  static_assert(NJ % 2 == 0, "tiles are transposed in pairs");
+  (void)S1;
   const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   const int row_l = el & 15;
-  const int col_l = 4 * (el >> 4);
+  const int q = el >> 4;
   const int n_base = kGateUp ? t_nt * (BN / 2) + wn * (WN / 2) : t_nt * BN + wn * WN;
 #pragma unroll
   for (int i = 0; i < MT16; ++i) {
     const int gm = wm * WM + i * 16 + row_l;
     const int srow = t_row0 + min(gm, t_rows - 1);
-    constexpr int NJ = kGateUp ? NT16 / 2 : NT16;
     float w = 1.0f;
     if (!kGateUp) w = bf16_bits_to_f32(row_w[srow]);
-    bf16_t* crow = C + (int64_t)srow * N + n_base + col_l;
+    const int64_t row_off = (int64_t)srow * N + n_base;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      bf16x4_t o, s0, s1;
+    for (int jp = 0; jp < NJ; jp += 2) {
+      bf16x4_t o[2], s0[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (kGateUp) {
-          s0[r] = (__bf16)acc[i][j][r];
-          s1[r] = (__bf16)acc[i][j + NJ][r];
-          const float g = (float)s0[r];
-          const float u = (float)s1[r];
-          const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
-          const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
-          o[r] = (__bf16)(u * sv);
-        } else {
-          s0[r] = (__bf16)acc[i][j][r];
-          o[r] = (__bf16)((float)s0[r] * w);
+      for (int h = 0; h < 2; ++h) {
+        const int j = jp + h;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s0[h][r] = (__bf16)acc[i][j][r];
+          if (kGateUp) {
+            const float g = (float)s0[h][r];
+            const float u = (float)(__bf16)acc[i][j + NJ][r];
+            const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
+            const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
+            o[h][r] = (__bf16)(u * sv);
+          } else {
+            o[h][r] = (__bf16)((float)s0[h][r] * w);
+          }
         }
-      }
-      if (gm < t_rows) {
-        *reinterpret_cast<bf16x4_t*>(crow + j * 16) = o;
-        if constexpr (kSave) {
-          const int64_t off = (crow - C) + j * 16;
-          if constexpr (kGateUp) {
+        if constexpr (kSave && kGateUp) {
+          // g and u in the accumulator layout: row r, column c of h -> 2 (r N + c)
+          if (gm < t_rows) {
             bf16x8_t gu;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) gu[r] = s0[r], gu[4 + r] = s1[r];
-            *reinterpret_cast<bf16x8_t*>(S0 + 2 * off) = gu;  // row r, column c of h -> 2 (r N + c)
-          } else {
-            *reinterpret_cast<bf16x4_t*>(S0 + off) = s0;
+            for (int r = 0; r < 4; ++r) gu[r] = s0[h][r], gu[4 + r] = (__bf16)acc[i][j + NJ][r];
+            *reinterpret_cast<bf16x8_t*>(S0 + 2 * (row_off + j * 16 + 4 * q)) = gu;
           }
+        }
+      }
+      transpose2(o);
+      if constexpr (kSave && !kGateUp) transpose2(s0);
+      if (gm < t_rows) {
+        bf16x8_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = o[0][r], v[4 + r] = o[1][r];
+        *reinterpret_cast<bf16x8_t*>(C + row_off + jp * 16 + 8 * q) = v;
+        if constexpr (kSave && !kGateUp) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = s0[0][r], v[4 + r] = s0[1][r];
+          *reinterpret_cast<bf16x8_t*>(S0 + row_off + jp * 16 + 8 * q) = v;
         }
       }
     }
