@@ -1,6 +1,7 @@
 // Device helpers shared by the CDNA4 matrix-core GEMMs (gfx950): operand
-// vector types, LDS DMA and its waits, the persistent XCD-aware tile walk
-// and the per-lane DMA chunk choice of the 16-byte LDS swizzle.
+// vector types, LDS DMA and its waits, the persistent XCD-aware tile walk,
+// the per-lane DMA chunk choice of the 16-byte LDS swizzle and the lane-group
+// transpose of the epilogues.
 #pragma once
 
 #include "moe_gemm.h"
@@ -113,6 +114,37 @@ struct DmaLane {
     return (chk0 & ~m) | (chk1 & m);
   }
 };
+
+// ---- epilogue stores ----
+
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// Cross-lane exchanges of gfx950 on 8-byte values (one per lane): swap32
+// trades lanes 32-63 of a for lanes 0-31 of b, swap16 trades the odd 16-lane
+// rows of a (lanes 16-31, 48-63) for the even rows of b. Lane l keeps its
+// l % 16 either way.
+__device__ __forceinline__ void swap32(bf16x4_t& a, bf16x4_t& b) {
+  const u32x2_t x = __builtin_bit_cast(u32x2_t, a), y = __builtin_bit_cast(u32x2_t, b);
+  const auto r0 = __builtin_amdgcn_permlane32_swap(x[0], y[0], false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap(x[1], y[1], false, false);
+  a = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[0], r1[0]});
+  b = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[1], r1[1]});
+}
+__device__ __forceinline__ void swap16(bf16x4_t& a, bf16x4_t& b) {
+  const u32x2_t x = __builtin_bit_cast(u32x2_t, a), y = __builtin_bit_cast(u32x2_t, b);
+  const auto r0 = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+  const auto r1 = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+  a = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[0], r1[0]});
+  b = __builtin_bit_cast(bf16x4_t, u32x2_t{r0[1], r1[1]});
+}
+// e[j] of lane (row r, group q = l / 16) holds columns 16 j + 4 q .. +3 of row
+// r (two 16-column tiles). Afterwards lane q holds columns 8 q .. 8 q + 7 of
+// the 32 (e[0] then e[1]): one 16-byte store, and the 4 lanes of a row cover
+// its 64 bytes contiguously.
+__device__ __forceinline__ void transpose2(bf16x4_t (&e)[2]) {
+  swap32(e[0], e[1]);
+  swap16(e[0], e[1]);
+}
 
 // ---- host side of the persistent launches ----
 

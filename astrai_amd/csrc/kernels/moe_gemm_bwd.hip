@@ -245,15 +245,22 @@ __device__ __forceinline__ float sigmoid_f(float g) {
 }
 
 // Epilogue from the accumulators (lane: row 16 i + l % 16, columns 16 j +
-// 4 (l / 16) .. + 3 of the wave's block), 8-byte stores.
+// 4 (l / 16) .. + 3 of the wave's block). The accumulators are rounded to
+// bf16 and, per pair of 16-column tiles, go through the lane-group transpose,
+// which leaves each lane 8 consecutive columns of its row; the elementwise
+// inputs (gu, the added gradient) are then read for exactly those columns
+// (16 / 32 contiguous bytes) and the outputs stored as 16-byte pieces. N is
+// a multiple of 8, so a lane's 8 columns are wholly inside the matrix or
+// wholly past its edge.
 template <Bwd kMode>
 __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16], const BwdArgs& p,
                                              const TileInfo& t, int wm, int wn) {
   constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16;
+  static_assert(NT16 % 2 == 0, "tiles are transposed in pairs");
   const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   const int row_l = el & 15;
-  const int col_l = 4 * (el >> 4);
-  const int n0 = t.nt * BwdCfg::BN + wn * BwdCfg::WN + col_l;
+  const int q = el >> 4;
+  const int nw = t.nt * BwdCfg::BN + wn * BwdCfg::WN;  // the wave's first column
 #pragma unroll
   for (int i = 0; i < MT16; ++i) {
     const int gm = wm * BwdCfg::WM + i * 16 + row_l;
@@ -268,37 +275,44 @@ __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][Bwd
       row_off = (int64_t)(t.row0 + min(gm, t.rows - 1)) * p.N;
     }
 #pragma unroll
-    for (int j = 0; j < NT16; ++j) {
-      const int n = n0 + j * 16;
-      if (!row_ok || n >= p.N) continue;
-      const int64_t off = row_off + n;
-      bf16x4_t o0;
-      if constexpr (kMode == Bwd::kDgradDown) {
-        const bf16x8_t gu = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off);
-        bf16x4_t o1;
+    for (int jp = 0; jp < NT16; jp += 2) {
+      bf16x4_t e[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float dh = (float)(__bf16)acc[i][j][r];
-          const float g = (float)gu[r];
-          const float u = (float)gu[4 + r];
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e[h][r] = (__bf16)acc[i][jp + h][r];
+      transpose2(e);
+      const int nn = nw + jp * 16 + 8 * q;  // the lane's 8 columns after the transpose
+      if (!row_ok || nn >= p.N) continue;
+      const int64_t off = row_off + nn;
+      bf16x8_t o0;
+      if constexpr (kMode == Bwd::kDgradDown) {
+        // gu keeps g[c..c+3], u[c..c+3] at 2 c: the lane's 8 columns are 32 contiguous bytes
+        const bf16x8_t gu0 = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off);
+        const bf16x8_t gu1 = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off + 8);
+        bf16x8_t o1;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const bf16x8_t& gu = c < 4 ? gu0 : gu1;
+          const float dh = (float)e[c >> 2][c & 3];
+          const float g = (float)gu[c & 3];
+          const float u = (float)gu[4 + (c & 3)];
           const float s = sigmoid_f(g);
           const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
-          o1[r] = (__bf16)(dh * act);                 // du
+          o1[c] = (__bf16)(dh * act);                 // du
           const float dact = (float)(__bf16)(dh * u);
-          o0[r] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
+          o0[c] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
         }
-        *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
-        *reinterpret_cast<bf16x4_t*>(p.c1 + off) = o1;
+        *reinterpret_cast<bf16x8_t*>(p.c1 + off) = o1;
       } else if constexpr (kMode == Bwd::kDgradInAdd) {
-        const bf16x4_t add = *reinterpret_cast<const bf16x4_t*>(p.e0 + off);
+        const bf16x8_t add = *reinterpret_cast<const bf16x8_t*>(p.e0 + off);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o0[r] = (__bf16)((float)(__bf16)acc[i][j][r] + (float)add[r]);
-        *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
+        for (int c = 0; c < 8; ++c) o0[c] = (__bf16)((float)e[c >> 2][c & 3] + (float)add[c]);
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o0[r] = (__bf16)acc[i][j][r];
-        *reinterpret_cast<bf16x4_t*>(p.c0 + off) = o0;
+        for (int c = 0; c < 8; ++c) o0[c] = e[c >> 2][c & 3];
       }
+      *reinterpret_cast<bf16x8_t*>(p.c0 + off) = o0;
     }
   }
 }
