@@ -39,7 +39,7 @@ PEAK_HBM_GBS = 8000.0
 # (it counts this part's 128-byte read requests as 64 bytes). Source:
 # profiles/moe_layer_d4096_f14336_e8_k2_t16384.md.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
-    "moe_bf16_d4096_f14336_e8_k2_t16384": (6395697.2 * 2 + 917597.0) * 1024,
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (6155562.2 * 2 + 917507.1) * 1024,
 }
 
 
