@@ -292,21 +292,24 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
     const int64_t row_off = (int64_t)srow * N + n_base;
 #pragma unroll
     for (int jp = 0; jp < NJ; jp += 2) {
-      bf16x4_t o[2], s0[2];
+      // gate/up: h = bf16(u * bf16(silu(g))) per element, then transposed;
+      // down: the rounded unweighted output is transposed and then scaled by
+      // the row's weight (the transpose keeps each lane's row)
+      bf16x4_t o[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int j = jp + h;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          s0[h][r] = (__bf16)acc[i][j][r];
+          const __bf16 a = (__bf16)acc[i][j][r];
           if (kGateUp) {
-            const float g = (float)s0[h][r];
+            const float g = (float)a;
             const float u = (float)(__bf16)acc[i][j + NJ][r];
             const float ex = __builtin_amdgcn_exp2f(g * -1.4426950408889634f);
             const float sv = (float)(__bf16)(g * __builtin_amdgcn_rcpf(1.0f + ex));
             o[h][r] = (__bf16)(u * sv);
           } else {
-            o[h][r] = (__bf16)((float)s0[h][r] * w);
+            o[h][r] = a;
           }
         }
         if constexpr (kSave && kGateUp) {
@@ -314,23 +317,22 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
           if (gm < t_rows) {
             bf16x8_t gu;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) gu[r] = s0[h][r], gu[4 + r] = (__bf16)acc[i][j + NJ][r];
+            for (int r = 0; r < 4; ++r) gu[r] = (__bf16)acc[i][j][r], gu[4 + r] = (__bf16)acc[i][j + NJ][r];
             *reinterpret_cast<bf16x8_t*>(S0 + 2 * (row_off + j * 16 + 4 * q)) = gu;
           }
         }
       }
       transpose2(o);
-      if constexpr (kSave && !kGateUp) transpose2(s0);
       if (gm < t_rows) {
         bf16x8_t v;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = o[0][r], v[4 + r] = o[1][r];
-        *reinterpret_cast<bf16x8_t*>(C + row_off + jp * 16 + 8 * q) = v;
-        if constexpr (kSave && !kGateUp) {
+        if constexpr (!kGateUp) {
+          if constexpr (kSave) *reinterpret_cast<bf16x8_t*>(S0 + row_off + jp * 16 + 8 * q) = v;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) v[r] = s0[0][r], v[4 + r] = s0[1][r];
-          *reinterpret_cast<bf16x8_t*>(S0 + row_off + jp * 16 + 8 * q) = v;
+          for (int c = 0; c < 8; ++c) v[c] = (__bf16)((float)v[c] * w);
         }
+        *reinterpret_cast<bf16x8_t*>(C + row_off + jp * 16 + 8 * q) = v;
       }
     }
   }
