@@ -53,6 +53,24 @@ def _expert_grads(x: Tensor, wg: Tensor, wu: Tensor, wd: Tensor, dz: Tensor | No
     return (z.detach(), grads) if z_out else grads
 
 
+class EmptyBatch(torch.autograd.Function):
+    """The layer on zero tokens with shared experts (mlp.py:64-100 on an empty
+    ``x``): an empty output whose gradient reaches ``x`` and the shared
+    experts' weights as zeros. The reference's routed output is then a plain
+    ``torch.zeros`` (every expert is skipped, mlp.py:89-94), so neither the
+    router nor the routed experts get a gradient."""
+
+    @staticmethod
+    def forward(ctx, x, *params):
+        ctx.param_specs = [(p.shape, p.dtype, p.device) for p in params]
+        return x.new_empty(0, x.shape[1])
+
+    @staticmethod
+    def backward(ctx, dout):
+        return (dout.new_zeros(0, dout.shape[1]),
+                *(torch.zeros(shape, dtype=dtype, device=device) for shape, dtype, device in ctx.param_specs))
+
+
 class RoutedExperts(torch.autograd.Function):
     """Routed experts and their weighted combine (mlp.py:89-100).
 

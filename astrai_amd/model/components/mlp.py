@@ -34,7 +34,7 @@ from torch import Tensor
 
 from astrai_amd.extension import ops
 from astrai_amd.factory import BaseFactory
-from astrai_amd.model.components.autograd import DenseExpert, RoutedExperts, routing_weights
+from astrai_amd.model.components.autograd import DenseExpert, EmptyBatch, RoutedExperts, routing_weights
 from astrai_amd.model.components.linear import Linear
 
 
@@ -236,7 +236,11 @@ class DeepSeekMoE(nn.Module):
         the router."""
         n_tokens = x.shape[0]
         if n_tokens == 0:
-            return x.new_empty(0, x.shape[1])
+            # the reference's routed output is a graph-less zeros here; only
+            # shared experts connect the output to x and to parameters
+            if self.n_shared_experts == 0:
+                return x.new_zeros(0, x.shape[1])
+            return EmptyBatch.apply(x, *[w for ws in self._expert_weights(self.shared_experts) for w in ws])
         t_routed, t_shared = self._weight_tables()
         routed_w = self._expert_weights(self.routed_experts)
         dim_ffn = routed_w[0][0].shape[0]

@@ -146,6 +146,49 @@ def test_moe_backward_workload_rows(gpu):
     _check_moe(layer, x, "d2048_f1408_e64_k6 t2048")
 
 
+@pytest.mark.parametrize("dim,dim_ffn,dtype,n_shared", [
+    (256, 384, torch.bfloat16, 1), (192, 320, torch.bfloat16, 2), (64, 96, torch.float32, 1),
+    (256, 384, torch.bfloat16, 0),
+])
+def test_moe_backward_zero_tokens(gpu, dim, dim_ffn, dtype, n_shared):
+    # an empty batch differentiates as autograd through the reference does: every routed expert is
+    # skipped, so only shared experts connect the output to x and to parameters (zero gradients);
+    # without them the output carries no graph at all
+    layer = _random_layer(gpu, dim, dim_ffn, 8, n_shared, 2, dtype)
+    x = torch.randn(2, 0, dim, device=gpu, dtype=dtype)
+    layer.requires_grad_(True)
+    layer.zero_grad(set_to_none=True)
+    xl = _leaf(x)
+    out = layer(xl)
+    assert out.shape == x.shape
+    if n_shared == 0:
+        rw = _leaf(layer.router.weight)
+        ref = R.moe_forward(_leaf(x), rw, None, [R.ExpertWeights(_leaf(m.gate.weight), _leaf(m.up.weight),
+                                                                  _leaf(m.down.weight)) for m in layer.routed_experts],
+                            [], layer.n_activated_experts)
+        assert not ref.requires_grad and not out.requires_grad
+        return
+    dout = torch.zeros_like(x)
+    ref_out, ref_dx, ref_drw, _, ref_exp, ref_shared = _oracle(layer, x, dout)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    assert xl.grad is not None and xl.grad.shape == x.shape
+
+    def same(got, want, label):
+        if want is None:
+            assert got is None, f"{label}: gradient where the reference has none"
+        else:
+            assert got is not None and got.shape == want.shape, f"{label}: missing gradient"
+            assert torch.equal(got, torch.zeros_like(got)), f"{label}: nonzero gradient from zero rows"
+
+    same(layer.router.weight.grad, ref_drw, "router.weight")
+    for group, mods, refs in (("expert", layer.routed_experts, ref_exp), ("shared", layer.shared_experts, ref_shared)):
+        for i, (m, r) in enumerate(zip(mods, refs)):
+            for name, got, want in (("gate", m.gate.weight.grad, r.gate.grad), ("up", m.up.weight.grad, r.up.grad),
+                                    ("down", m.down.weight.grad, r.down.grad)):
+                same(got, want, f"{group}{i}.{name}")
+
+
 @pytest.mark.parametrize("dim,dim_ffn", [(192, 320), (256, 384)])  # recompute / grouped backward kernels
 def test_mlp_backward(gpu, dim, dim_ffn):
     torch.manual_seed(1)

@@ -89,6 +89,20 @@ def _random_layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, seed=0):
     return layer
 
 
+@pytest.mark.parametrize("dim,dim_ffn,dtype", [(256, 384, torch.bfloat16), (64, 96, torch.float32)])
+def test_zero_tokens(gpu, dim, dim_ffn, dtype):
+    # an empty batch runs every stage on zero rows and returns an empty output (mlp.py:64-72)
+    layer = _random_layer(gpu, dim, dim_ffn, 8, 1, 2, dtype)
+    x = torch.randn(2, 0, dim, device=gpu, dtype=dtype)
+    with torch.no_grad():
+        out = layer(x)
+    torch.cuda.synchronize()
+    assert out.shape == x.shape and out.dtype == dtype
+    # like the reference, which unpacks (bsz, seq_len, dim) first, a 2-D input is refused
+    with pytest.raises(ValueError):
+        layer(torch.randn(0, dim, device=gpu, dtype=dtype))
+
+
 @pytest.mark.parametrize("dim,dim_ffn,n_exp,n_shared,top_k,dtype", [
     (8, 16, 4, 1, 2, torch.bfloat16),  # the reference's tiny MoE test config
     (8, 16, 4, 1, 2, torch.float32),
