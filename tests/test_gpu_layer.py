@@ -90,6 +90,35 @@ def _random_layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, seed=0):
 
 
 @pytest.mark.parametrize("dim,dim_ffn,dtype", [(256, 384, torch.bfloat16), (64, 96, torch.float32)])
+def test_non_finite_tokens_stay_contained(gpu, dim, dim_ffn, dtype):
+    # a token whose input holds NaN / inf has non-finite router logits, so the reference's softmax
+    # makes its whole probability row NaN; which experts torch.topk then names is its own ordering
+    # detail, but the token's output is NaN either way. Every other token is unaffected: routing
+    # bit-exact, outputs within tolerance.
+    layer = _random_layer(gpu, dim, dim_ffn, 8, 1, 2, dtype)
+    g = torch.Generator(device=gpu).manual_seed(9)
+    x = torch.randn(1, 64, dim, generator=g, device=gpu).to(dtype)
+    bad = [5, 9, 40]
+    x[0, 5, 3] = float("nan")
+    x[0, 9, 0] = float("inf")
+    x[0, 40, :] = float("-inf")
+    with torch.no_grad():
+        out = layer(x)
+        rw, rb, experts, shared = R.module_weights(layer)
+        xf = x.view(-1, dim)
+        trace = R.routed_forward(xf, rw, rb, experts, layer.n_activated_experts, trace=True)
+        ref = (R.shared_forward(xf, shared) + trace.out).view_as(x)
+    torch.cuda.synchronize()
+    assert torch.isnan(ref[0, bad]).all() and torch.isnan(out[0, bad]).all()
+    good = [t for t in range(64) if t not in bad]
+    res = ops.moe_route(trace.logits, layer.n_activated_experts)
+    assert torch.equal(res.topk_idx[good].long().sort(-1).values, trace.topk_idx[good].sort(-1).values)
+    assert torch.equal(res.topk_w[good], trace.topk_w[good])
+    rtol, atol = _tol(dtype)
+    torch.testing.assert_close(out[0, good].float(), ref[0, good].float(), rtol=rtol, atol=(2 + 1) * atol)
+
+
+@pytest.mark.parametrize("dim,dim_ffn,dtype", [(256, 384, torch.bfloat16), (64, 96, torch.float32)])
 def test_zero_tokens(gpu, dim, dim_ffn, dtype):
     # an empty batch runs every stage on zero rows and returns an empty output (mlp.py:64-72)
     layer = _random_layer(gpu, dim, dim_ffn, 8, 1, 2, dtype)
