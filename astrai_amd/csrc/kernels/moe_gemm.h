@@ -12,6 +12,10 @@ namespace astrai_moe {
 // kernel compute-bound on empty rows.
 constexpr int kMfmaBigBM = 256;
 constexpr int kMfmaSmallBM = 32;
+// Mid-sized expert loads (about 48-128 rows per expert): one 64-row tile per
+// expert reads its weights once, where 32-row tiles would stream them twice or
+// more and 256-row tiles would compute mostly padding.
+constexpr int kMfmaMidBM = 64;
 
 // Shape constraints of the bf16 kernels: K a multiple of 64, the output
 // columns a multiple of the column tile, 16-byte aligned operands.

@@ -740,6 +740,10 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
 // Decode tiles: 32 x 256 outputs, 4 waves of 32 x 64, four stages in flight
 // to keep the expert-weight stream busy; every wave issues DMA.
 using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8>;
+// Mid tiles: 64 x 256 outputs, 8 waves of 32 x 64 (the decode wave tile, two
+// rows of waves), three stages in flight: 3 x 40 KB of stages + the waves'
+// epilogue slices fit the 160 KB of LDS.
+using MidCfg = TileCfg<kMfmaMidBM, 256, 3, 2, 4, 8>;
 static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfmaBigBM, "prefill tile height");
 
 template <bool kGateUp, bool kPacked, bool kSave = false, bool kGather = false>
@@ -776,6 +780,8 @@ int gate_up_dispatch(const void* x_perm, const int32_t* tiles, int64_t capacity,
                      const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, void* h, hipStream_t s) {
   if (block_m == kMfmaBigBM)
     return launch_stream<true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
+  if (block_m == kMfmaMidBM)
+    return launch<MidCfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
   return launch<SmallCfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
 }
 
@@ -784,6 +790,8 @@ int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const v
                   const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, void* y, hipStream_t s) {
   if (block_m == kMfmaBigBM)
     return launch_stream<false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
+  if (block_m == kMfmaMidBM)
+    return launch<MidCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
   return launch<SmallCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
 }
 
@@ -791,13 +799,13 @@ int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const v
 
 bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m, const void* a, const void* c) {
   // 32-bit DMA offsets: a tile spans at most 256 rows of K * 2 bytes
-  return (block_m == kMfmaBigBM || block_m == kMfmaSmallBM) && dim % kBK == 0 && dim_ffn % 128 == 0 &&
-         dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
+  return (block_m == kMfmaBigBM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) && dim % kBK == 0 &&
+         dim_ffn % 128 == 0 && dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m, const void* a, const void* c) {
-  return (block_m == kMfmaBigBM || block_m == kMfmaSmallBM) && dim_ffn % kBK == 0 && dim % 256 == 0 &&
-         dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
+  return (block_m == kMfmaBigBM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) && dim_ffn % kBK == 0 &&
+         dim % 256 == 0 && dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
@@ -834,6 +842,9 @@ int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token, const
   if (block_m == kMfmaBigBM)
     return launch_stream<true, false, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
                                                    nullptr, nullptr, sorted_token);
+  if (block_m == kMfmaMidBM)
+    return launch<MidCfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
+                                             sorted_token);
   return launch<SmallCfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
                                              sorted_token);
 }

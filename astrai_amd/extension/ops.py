@@ -86,6 +86,16 @@ def _require_gpu(t: torch.Tensor, name: str, ndim: int | None = None) -> None:
         raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
 
 
+def _require_table(t: torch.Tensor, name: str, n_experts: int, like: torch.Tensor) -> None:
+    """A weight argument of the GEMMs is a device array of ``n_experts``
+    pointers (``expert_weight_table``); the kernels dereference its entries,
+    so a weight tensor passed in its place must stop here."""
+    _require_gpu(t, name, 1)
+    if t.dtype != torch.int64 or t.numel() != n_experts or t.device != like.device:
+        raise ValueError(f"{name} must be an int64 pointer table of {n_experts} entries on {like.device} "
+                         f"(expert_weight_table), got {t.dtype} shape {tuple(t.shape)} on {t.device}")
+
+
 def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -192,6 +202,9 @@ def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Te
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
+    _require_table(w_gate, "w_gate", n_experts, x_perm)
+    if not packed:
+        _require_table(w_up, "w_up", n_experts, x_perm)
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     if packed:
         _check(
@@ -232,6 +245,8 @@ def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: 
     code = _dtype_code(x, "x")
     n_tokens, dim = x.shape
     n_rows = sorted_token.numel()
+    _require_table(w_gate, "w_gate", n_experts, x)
+    _require_table(w_up, "w_up", n_experts, x)
     h = torch.empty(n_rows, dim_ffn, dtype=x.dtype, device=x.device)
     _check(
         loader.library().astrai_moe_gemm_gate_up_gather(
@@ -254,6 +269,7 @@ def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, so
     n_rows, dim_ffn = h.shape
     if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
         raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    _require_table(w_down, "w_down", n_experts, h)
     y = _out_buffer(out, n_rows, dim, h)
     if packed:
         _check(
@@ -408,6 +424,8 @@ def moe_gemm_gate_up_train(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: to
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
+    _require_table(w_gate, "w_gate", n_experts, x_perm)
+    _require_table(w_up, "w_up", n_experts, x_perm)
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     gu = torch.empty(n_rows, 2 * dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     _lib_call("astrai_moe_gemm_gate_up_train", x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
@@ -431,6 +449,7 @@ def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tens
     n_rows, dim_ffn = h.shape
     if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
         raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    _require_table(w_down, "w_down", n_experts, h)
     y, y_unw = (torch.empty(n_rows, dim, dtype=h.dtype, device=h.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_down_train", h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
               sorted_w.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, TRAIN_BLOCK_M, y.data_ptr(),
@@ -462,6 +481,7 @@ def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Ten
     code = _dtype_code(dy, "dy")
     n_rows, dim = dy.shape
     dim_ffn = gu.shape[1] // 2
+    _require_table(w_down, "w_down", n_experts, dy)
     dg, du = (torch.empty(n_rows, dim_ffn, dtype=dy.dtype, device=dy.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_dgrad_down", dy.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
               gu.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, dg.data_ptr(), du.data_ptr(),
@@ -475,6 +495,8 @@ def moe_gemm_dgrad_gate_up(dg: torch.Tensor, du: torch.Tensor, tiles: torch.Tens
     _require_gpu(dg, "dg", 2)
     code = _dtype_code(dg, "dg")
     n_rows, dim_ffn = dg.shape
+    _require_table(w_gate, "w_gate", n_experts, dg)
+    _require_table(w_up, "w_up", n_experts, dg)
     dx = torch.empty(n_rows, dim, dtype=dg.dtype, device=dg.device)
     _lib_call("astrai_moe_gemm_dgrad_gate_up", dg.data_ptr(), du.data_ptr(), tiles.data_ptr(), tiles.numel(),
               w_gate.data_ptr(), w_up.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, TRAIN_BLOCK_M,

@@ -257,8 +257,8 @@ def main():
     bytes_combine = rows * w.dim * s + T * w.dim * s + rows * (s + 8)
     traffic = MEASURED_TRAFFIC_BYTES.get(name)
     block_m = ops.select_block_m(T, w.n_experts, w.top_k, w.dim, w.dim_ffn, w.dtype)
-    if bf16 and block_m == 32:
-        # decode-sized loads: the gate/up kernel streams the routed experts' weights
+    if bf16 and block_m in (32, 64):
+        # decode- and mid-sized loads: the gate/up kernel streams the routed experts' weights
         gu_bytes = n_active * 2.0 * w.dim * w.dim_ffn * s + rows * w.dim * s + rows * w.dim_ffn * s
         gbs = gu_bytes / t_gu / 1e9
         roofline = {"kernel": "gemm_mfma_kernel<gate_up" + (", gather>" if gathered else ">"), "bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,

@@ -181,7 +181,7 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
 
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
     (2048, 8, 2, 1024, 1536),  # 256-row tiles
-    (300, 16, 4, 512, 256),  # 32-row tiles
+    (300, 16, 4, 512, 256),  # 64-row tiles
     (64, 128, 8, 4096, 1536),  # decode-sized loads, some experts empty
     (16384, 4, 2, 256, 128),  # many rows per expert, several tiles per workgroup
     (1, 8, 2, 256, 128),  # one token
@@ -196,7 +196,7 @@ def test_gate_up_gather_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
     experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=14)
     bm = ops.select_block_m(n_tok, n_exp, top_k, dim, dim_ffn, dtype)
-    assert bm in (32, 256)
+    assert bm in (32, 64, 256)
     perm = ops.moe_permute(route, x, n_exp, bm)
     idx = ops.moe_permute(route, x, n_exp, bm, copy_rows=False)
     assert idx.x_perm is None
@@ -235,6 +235,7 @@ def _packed_layout(w0, w1, tile_rows):
     (600, 2, 2, 1024, 65536, 256),  # down K = 65536: 128 KB weight rows, 32 MB per 256-row tile
     (300, 2, 1, 65536, 256, 256),  # gate/up K = 65536
     (64, 2, 2, 65536, 512, 32),  # the 32-row kernels at the same K
+    (128, 2, 2, 65536, 512, 64),  # the 64-row kernels at the same K
 ])
 def test_long_k_rows(gpu, n_tok, n_exp, top_k, dim, dim_ffn, block_m):
     # byte offsets within a tile grow with K (rows x K x 2 bytes, 32-bit in the
@@ -242,7 +243,9 @@ def test_long_k_rows(gpu, n_tok, n_exp, top_k, dim, dim_ffn, block_m):
     dtype = torch.bfloat16
     route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=31)
     g = torch.Generator(device=gpu).manual_seed(32)
-    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    # x scaled so the gate pre-activation keeps its K = 4096 spread (std 1.3): at std 5, a one-ulp bf16 rounding
+    # flip of g (fp32 sums in another order) is amplified ~6x by silu at g ~ -5, past the bf16 tolerance
+    x = (torch.randn(n_tok, dim, generator=g, device=gpu) * min(1.0, (4096 / dim) ** 0.5)).to(dtype)
     experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=33)
     perm = ops.moe_permute(route, x, n_exp, block_m)
     tg = ops.expert_weight_table([e.gate for e in experts], (dim_ffn, dim))
@@ -256,10 +259,12 @@ def test_long_k_rows(gpu, n_tok, n_exp, top_k, dim, dim_ffn, block_m):
         a, b = offs[e], offs[e + 1]
         if a == b:
             continue
-        xe = perm.x_perm[a:b]
-        h_ref = F.linear(xe, w.up) * F.silu(F.linear(xe, w.gate))  # mlp.py:23
-        torch.testing.assert_close(h[a:b], h_ref, **BF16_TOL)
-        y_ref = F.linear(h[a:b], w.down) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
+        # fp32 sums rounded to bf16 at the reference's rounding points (mlp.py:23-24, :97)
+        xe = perm.x_perm[a:b].float()
+        g = F.linear(xe, w.gate.float()).to(dtype)
+        u = F.linear(xe, w.up.float()).to(dtype)
+        torch.testing.assert_close(h[a:b], u * F.silu(g), **BF16_TOL)
+        y_ref = F.linear(h[a:b].float(), w.down.float()).to(dtype) * perm.sorted_w[a:b].unsqueeze(-1)
         torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
 
 
@@ -303,11 +308,14 @@ def test_packed_gemms_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     (2048, 8, 2, 1024, 1280),  # many row tiles per expert, several tiles per workgroup
     (700, 16, 4, 2048, 768),  # ragged row tiles
     (1, 8, 2, 1024, 1024),  # one token
+    (512, 8, 1, 1024, 512),  # 64 rows per expert: one 64-row tile each
 ])
-def test_decode_gemms_row_strided_packed_gathered_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
-    # 32-row tiles: row-strided, packed and gathered operands give equal bits,
-    # and every expert's rows match torch
-    dtype, bm = torch.bfloat16, 32
+@pytest.mark.parametrize("bm", [32, 64])
+def test_decode_gemms_row_strided_packed_gathered_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn, bm):
+    # 32- and 64-row tiles: row-strided, packed and gathered operands give
+    # equal bits, the two tile heights give equal bits (the same per-wave MFMA
+    # sequence over K), and every expert's rows match torch
+    dtype = torch.bfloat16
     route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=21)
     g = torch.Generator(device=gpu).manual_seed(22)
     x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
@@ -325,10 +333,18 @@ def test_decode_gemms_row_strided_packed_gathered_bit_identical(gpu, n_tok, n_ex
     tpd = ops.expert_weight_table(pd, (dim, dim_ffn))
     hp = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tpg, tpg, n_exp, dim_ffn, bm, packed=True)
     yp = ops.moe_gemm_down(h, perm.tiles, tpd, perm.sorted_w, n_exp, dim, bm, packed=True)
+    if bm != 32:
+        p32 = ops.moe_permute(route, x, n_exp, 32)
+        h32 = ops.moe_gemm_gate_up(p32.x_perm, p32.tiles, tg, tu, n_exp, dim_ffn, 32)
+        y32 = ops.moe_gemm_down(h32, p32.tiles, td, p32.sorted_w, n_exp, dim, 32)
     torch.cuda.synchronize()
     assert torch.equal(h, hp)
     assert torch.equal(hg, hp)
     assert torch.equal(y, yp)
+    if bm != 32:
+        assert torch.equal(p32.sorted_token, perm.sorted_token)
+        assert torch.equal(h32, h)
+        assert torch.equal(y32, y)
     # and against torch, per expert (first rows of the output only where rows exist)
     offs = perm.expert_offsets.tolist()
     for e in range(n_exp):

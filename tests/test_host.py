@@ -230,16 +230,31 @@ def test_block_m_policy():
     bf = torch.bfloat16
     assert ops.select_block_m(16384, 8, 2, 4096, 14336, bf) == 256
     assert ops.select_block_m(64, 128, 8, 4096, 1536, bf) == 32
-    assert ops.select_block_m(1024, 8, 2, 512, 1024, torch.float32) == 64
+    assert ops.select_block_m(1024, 8, 2, 512, 1024, torch.float32) == 64  # the general kernel's tiles
     assert ops.select_block_m(100, 4, 2, 8, 16, bf) == 64  # shapes the MFMA kernels do not tile
+    # routed, by average rows per expert: 32-row tiles below 24, 64-row tiles below 96, then 256
+    assert ops.select_block_m(368, 128, 8, 4096, 1536, bf) == 32  # 23 rows per expert
+    assert ops.select_block_m(384, 128, 8, 4096, 1536, bf) == 64  # 24
+    assert ops.select_block_m(1520, 128, 8, 4096, 1536, bf) == 64  # 95
+    assert ops.select_block_m(1536, 128, 8, 4096, 1536, bf) == 256  # 96
+    assert ops.select_block_m(383, 8, 2, 4096, 14336, bf) == 64
+    assert ops.select_block_m(384, 8, 2, 4096, 14336, bf) == 256
+    # one dense MLP (shared experts): 32 below 96 tokens, 256 once T * (F/128 + D/256) >= 65536
+    assert ops.select_block_m(95, 1, 1, 2048, 2816, bf) == 32
+    assert ops.select_block_m(96, 1, 1, 2048, 2816, bf) == 64
+    assert ops.select_block_m(2184, 1, 1, 2048, 2816, bf) == 64  # 30 column tiles per row tile
+    assert ops.select_block_m(2185, 1, 1, 2048, 2816, bf) == 256
+    assert ops.select_block_m(511, 1, 1, 4096, 14336, bf) == 64  # 128 column tiles per row tile
+    assert ops.select_block_m(512, 1, 1, 4096, 14336, bf) == 256
+    assert ops.select_block_m(16384, 1, 1, 2048, 2816, bf) == 256
 
 
 def test_packed_weights_follow_the_matrix_core_policy():
     # the layer packs exactly the shapes the matrix-core kernels take
     for dim, dim_ffn in [(4096, 14336), (2048, 1408), (256, 512), (512, 256), (96, 80), (8, 16), (256, 64)]:
         for dtype in (torch.bfloat16, torch.float32):
-            bm = ops.select_block_m(1024, 8, 2, dim, dim_ffn, dtype)
-            assert ops.packed_supported(dim, dim_ffn, dtype) == (bm in (32, 256)), (dim, dim_ffn, dtype)
+            bm = ops.select_block_m(1024, 8, 2, dim, dim_ffn, dtype)  # 256 rows per expert: 256-row MFMA tiles
+            assert ops.packed_supported(dim, dim_ffn, dtype) == (bm == 256), (dim, dim_ffn, dtype)
     m = DeepSeekMoE(512, 256, 4, n_shared_experts=0)
     assert not m.pack_weights and not m.uses_packed_weights(torch.bfloat16)  # opt-in
     m.pack_weights = True
@@ -252,3 +267,72 @@ def test_ops_validate_before_launch():
         ops.moe_route(torch.zeros(4, 8), 2)
     with pytest.raises(ValueError):
         ops.expert_weight_table([], (2, 2))
+
+
+# -- weight-table arguments ---------------------------------------------------
+
+
+class _NoLaunch:
+    """Stands in for the library: reaching it means a wrapper let its
+    arguments through to a launch."""
+
+    def __getattr__(self, name):
+        raise AssertionError(f"reached the library ({name})")
+
+    def library(self):
+        return self
+
+
+def _table_wrappers(x, tiles, n_exp, dim, dim_ffn):
+    """Each wrapper that takes weight tables, as ``f(gate, up, down)``."""
+    rows = x.shape[0]
+    h = torch.zeros(rows, dim_ffn, dtype=x.dtype)
+    w = torch.ones(rows, dtype=x.dtype)
+    gu = torch.zeros(rows, 2 * dim_ffn, dtype=x.dtype)
+    sorted_token = torch.arange(rows, dtype=torch.int32)
+    return {
+        "gate_up": lambda g, u, d: ops.moe_gemm_gate_up(x, tiles, g, u, n_exp, dim_ffn, 32),
+        "gate_up_packed": lambda g, u, d: ops.moe_gemm_gate_up(x, tiles, g, u, n_exp, dim_ffn, 32, packed=True),
+        "gate_up_gather": lambda g, u, d: ops.moe_gemm_gate_up_gather(x, sorted_token, tiles, g, u, n_exp, dim_ffn, 32),
+        "down": lambda g, u, d: ops.moe_gemm_down(h, tiles, d, w, n_exp, dim, 32),
+        "down_packed": lambda g, u, d: ops.moe_gemm_down(h, tiles, d, w, n_exp, dim, 32, packed=True),
+        "gate_up_train": lambda g, u, d: ops.moe_gemm_gate_up_train(x, tiles, g, u, n_exp, dim_ffn),
+        "down_train": lambda g, u, d: ops.moe_gemm_down_train(h, tiles, d, w, n_exp, dim),
+        "dgrad_down": lambda g, u, d: ops.moe_gemm_dgrad_down(x, tiles, d, gu, n_exp),
+        "dgrad_gate_up": lambda g, u, d: ops.moe_gemm_dgrad_gate_up(h, h, tiles, g, u, n_exp, dim),
+    }
+
+
+def test_weight_tables_are_checked_before_any_launch(monkeypatch):
+    # the kernels dereference every table entry: a weight tensor, a table of
+    # the wrong length or dtype passed in a table's place must raise on the
+    # host, never reach a launch (device placement relaxed to run on the CPU)
+    def relaxed(t, name, ndim=None):
+        if not isinstance(t, torch.Tensor) or not t.is_contiguous() or (ndim is not None and t.dim() != ndim):
+            raise ValueError(name)
+
+    monkeypatch.setattr(ops, "_require_gpu", relaxed)
+    monkeypatch.setattr(ops, "_kernel", lambda name: lambda *args: _NoLaunch().__getattr__(name))
+    monkeypatch.setattr(ops, "loader", _NoLaunch())
+    monkeypatch.setattr(ops, "_stream", lambda t: 0)
+    n_exp, dim, dim_ffn, bf = 4, 256, 128, torch.bfloat16
+    x = torch.zeros(64, dim, dtype=bf)
+    tiles = torch.zeros(64, dtype=torch.int32)
+    good = torch.zeros(n_exp, dtype=torch.int64)
+    bad = {
+        "weight tensor": torch.zeros(dim_ffn, dim, dtype=bf),
+        "too few entries": torch.zeros(n_exp - 1, dtype=torch.int64),
+        "too many entries": torch.zeros(n_exp + 1, dtype=torch.int64),
+        "int32 entries": torch.zeros(n_exp, dtype=torch.int32),
+    }
+    for name, call in _table_wrappers(x, tiles, n_exp, dim, dim_ffn).items():
+        with pytest.raises(AssertionError, match="reached the library"):
+            call(good, good, good)  # valid tables get through to the launch
+        for what, t in bad.items():
+            for pos in range(3):
+                args = [good, good, good]
+                args[pos] = t
+                if (name.endswith("packed") and pos == 1) or (pos == 2) != (name.startswith("down") or name == "dgrad_down"):
+                    continue  # an argument this wrapper does not read
+                with pytest.raises(ValueError, match=r"^w_(gate|up|down)"):
+                    call(*args)
