@@ -113,7 +113,8 @@ __global__ __launch_bounds__(kGenThreads) void gemm_generic_kernel(
           const float s = Elem<T>::round(silu_f32(g));
           v = u * s;
         } else {
-          v = Elem<T>::round(acc0[i][j]) * Elem<T>::to_f32(row_w[row0 + r]);
+          // no row weights (a dense expert): weight 1, an exact product
+          v = Elem<T>::round(acc0[i][j]) * (row_w ? Elem<T>::to_f32(row_w[row0 + r]) : 1.0f);
         }
         C[(row0 + r) * N + n] = Elem<T>::from_f32(v);
       }
@@ -219,7 +220,7 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                         n_experts, dim_ffn, dim, block_m, y);
   if (rc) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
-  ASTRAI_REQUIRE(w_down && sorted_w, "gemm_down: null weight table or row weights");
+  ASTRAI_REQUIRE(w_down, "gemm_down: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == ASTRAI_MOE_BF16) {
@@ -293,7 +294,7 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
                  "gemm_down_packed: unsupported shape (dim_ffn %lld, dim %lld, block_m %d) or alignment",
                  (long long)dim_ffn, (long long)dim, block_m);
   if (n_rows == 0) return ASTRAI_MOE_OK;
-  ASTRAI_REQUIRE(w_packed && sorted_w, "gemm_down_packed: null weight table or row weights");
+  ASTRAI_REQUIRE(w_packed, "gemm_down_packed: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   return launch_mfma_down(h, tiles, capacity, w_packed, sorted_w, dim_ffn, dim, block_m, true, y,
                           static_cast<hipStream_t>(stream));

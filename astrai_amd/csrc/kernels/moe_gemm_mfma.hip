@@ -195,7 +195,7 @@ __device__ __forceinline__ void store_tile(f32x4_t (&acc)[WM / 16][WN / 16], cha
     const int srow = t_row0 + min(gmr, t_rows - 1);
     constexpr int NJ = kGateUp ? NT16 / 2 : NT16;
     float w = 1.0f;
-    if (!kGateUp) w = bf16_bits_to_f32(row_w[srow]);
+    if (!kGateUp && row_w != nullptr) w = bf16_bits_to_f32(row_w[srow]);  // no row weights: 1
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       bf16x4_t o;
@@ -288,7 +288,7 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
     const int gm = wm * WM + i * 16 + row_l;
     const int srow = t_row0 + min(gm, t_rows - 1);
     float w = 1.0f;
-    if (!kGateUp) w = bf16_bits_to_f32(row_w[srow]);
+    if (!kGateUp && row_w != nullptr) w = bf16_bits_to_f32(row_w[srow]);  // no row weights: 1
     const int64_t row_off = (int64_t)srow * N + n_base;
 #pragma unroll
     for (int jp = 0; jp < NJ; jp += 2) {

@@ -221,6 +221,33 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   }
 }
 
+// Tile list of one dense expert over n_rows rows (expert 0 owns every row),
+// for running the shared experts and the standalone MLP on the grouped GEMMs;
+// optionally the matching expert offsets {0, n_rows}. Built on the device so
+// that a captured graph owns it like any other output of the forward.
+__global__ __launch_bounds__(256) void dense_tiles_kernel(
+    int64_t n_rows, int block_m, int64_t tile_capacity,
+    int32_t* __restrict__ tiles, int32_t* __restrict__ offsets) {
+  const int64_t n_tiles = ceil_div(n_rows, block_m);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) {
+    tiles[0] = (int32_t)n_tiles;
+    tiles[1] = block_m;
+    tiles[2] = (int32_t)tile_capacity;
+    tiles[3] = 0;
+    if (offsets != nullptr) {
+      offsets[0] = 0;
+      offsets[1] = (int32_t)n_rows;
+    }
+  }
+  if (i < n_tiles) {
+    int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER + i * ASTRAI_MOE_TILE_STRIDE;
+    t[0] = 0;
+    t[1] = (int32_t)(i * block_m);
+    t[2] = (int32_t)n_rows;
+  }
+}
+
 template <typename T>
 int launch_permute(const int32_t* topk_idx, const void* topk_w,
                    const int32_t* chunk_hist, const void* x, int64_t n_tokens,
@@ -316,4 +343,27 @@ extern "C" int astrai_moe_permute(
                                  sorted_token, sorted_w, token_pos, x_perm, tiles,
                                  capacity, chunk_base, s);
   return fail(ASTRAI_MOE_EINVAL, "permute: unsupported dtype %d", dtype);
+}
+
+extern "C" int astrai_moe_dense_tiles(int64_t n_rows, int block_m,
+                                      int32_t* tiles, int64_t tiles_len,
+                                      int32_t* expert_offsets, void* stream) {
+  clear_error();
+  ASTRAI_REQUIRE(n_rows >= 0 && n_rows < (1ll << 31),
+                 "dense_tiles: n_rows must be in [0, 2^31) (got %lld)",
+                 (long long)n_rows);
+  ASTRAI_REQUIRE(block_m >= 1, "dense_tiles: block_m must be >= 1");
+  const int64_t need = astrai_moe_tile_list_len(n_rows, 1, 1, block_m);
+  ASTRAI_REQUIRE(tiles_len >= need,
+                 "dense_tiles: tile list holds %lld int32, needs %lld",
+                 (long long)tiles_len, (long long)need);
+  ASTRAI_REQUIRE(tiles != nullptr, "dense_tiles: null tile list");
+  const int64_t capacity =
+      (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
+  const int64_t n_tiles = ceil_div(n_rows, block_m);
+  const int64_t grid = n_tiles > 0 ? ceil_div(n_tiles, 256) : 1;
+  hipLaunchKernelGGL(dense_tiles_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), n_rows, block_m,
+                     capacity, tiles, expert_offsets);
+  return check_launch("dense_tiles_kernel");
 }

@@ -30,7 +30,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 KERNEL_NAMES = ["moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_down", "moe_combine"]
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LIB_PATH = Path(os.environ.get("ASTRAI_MOE_LIB", Path(__file__).resolve().parent / "libastrai_moe.so"))
 
 _c_i32p = ctypes.POINTER(ctypes.c_int32)
@@ -44,6 +44,7 @@ _SIGNATURES: dict[str, tuple] = {
     "astrai_moe_last_error": (ctypes.c_char_p, []),
     "astrai_moe_select_block_m": (_int, [_i64, _int, _int, _i64, _i64, _int]),
     "astrai_moe_tile_list_len": (_i64, [_i64, _int, _int, _int]),
+    "astrai_moe_dense_tiles": (_int, [_i64, _int, _vp, _i64, _vp, _vp]),
     "astrai_moe_route": (_int, [_vp, _int, _i64, _int, _int, _vp, _vp, _vp, _vp]),
     "astrai_moe_permute": (
         _int,

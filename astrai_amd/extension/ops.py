@@ -100,6 +100,28 @@ def _ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def _tag_tiles(tiles: torch.Tensor, block_m: int) -> torch.Tensor:
+    """Record the row-tile height a tile list was built for. The list's own
+    header holds it on the device, where the host cannot read it without a
+    synchronisation; the GEMM wrappers compare this tag with their
+    ``block_m``."""
+    tiles._astrai_block_m = block_m
+    return tiles
+
+
+def _check_tiles(tiles: torch.Tensor, block_m: int, like: torch.Tensor, who: str) -> None:
+    """A tile list must be a device int32 list built for this ``block_m``: a
+    list of 256-row tiles run with 64-row tiles would compute only the first 64
+    rows of each tile and leave the rest of the output unwritten."""
+    _require_gpu(tiles, f"{who}: tiles", 1)
+    if tiles.dtype != torch.int32 or tiles.device != like.device or tiles.numel() < TILE_HEADER:
+        raise ValueError(f"{who}: tiles must be an int32 tile list on {like.device} "
+                         f"(got {tiles.dtype}, {tiles.numel()} entries on {tiles.device})")
+    built = getattr(tiles, "_astrai_block_m", None)
+    if built is not None and built != block_m:
+        raise ValueError(f"{who}: the tile list was built for block_m {built}, called with block_m {block_m}")
+
+
 def select_block_m(n_tokens: int, n_experts: int, top_k: int, dim: int, dim_ffn: int, dtype: torch.dtype) -> int:
     """Rows per GEMM tile the kernels use for this problem (host policy)."""
     code = _DTYPE_CODES.get(dtype)
@@ -189,7 +211,7 @@ def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: in
            token_pos.data_ptr(), _ptr(x_perm), tiles.data_ptr(), tl, chunk_base.data_ptr(), _stream(x)),
         "moe_permute",
     )
-    return PermuteResult(offsets, sorted_token, sorted_w, token_pos, x_perm, tiles, block_m)
+    return PermuteResult(offsets, sorted_token, sorted_w, token_pos, x_perm, _tag_tiles(tiles, block_m), block_m)
 
 
 def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
@@ -202,6 +224,7 @@ def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Te
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
+    _check_tiles(tiles, block_m, x_perm, "moe_gemm_gate_up")
     _require_table(w_gate, "w_gate", n_experts, x_perm)
     if not packed:
         _require_table(w_up, "w_up", n_experts, x_perm)
@@ -245,6 +268,7 @@ def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: 
     code = _dtype_code(x, "x")
     n_tokens, dim = x.shape
     n_rows = sorted_token.numel()
+    _check_tiles(tiles, block_m, x, "moe_gemm_gate_up_gather")
     _require_table(w_gate, "w_gate", n_experts, x)
     _require_table(w_up, "w_up", n_experts, x)
     h = torch.empty(n_rows, dim_ffn, dtype=x.dtype, device=x.device)
@@ -257,30 +281,34 @@ def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: 
     return h
 
 
-def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
+def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor | None,
                   n_experts: int, dim: int, block_m: int, out: torch.Tensor | None = None,
                   packed: bool = False) -> torch.Tensor:
     """y = down(h) * routing weight over every expert's rows (mlp.py:24, :97).
 
+    ``sorted_w`` None: no routing weight (a dense expert, mlp.py:24 alone).
     ``packed``: ``w_down`` is a table of packed copies (``moe_pack_down``)."""
     fn = _kernel("moe_gemm_down")
     _require_gpu(h, "h", 2)
     code = _dtype_code(h, "h")
     n_rows, dim_ffn = h.shape
-    if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
-        raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    if sorted_w is not None:
+        _require_gpu(sorted_w, "sorted_w")
+        if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype or sorted_w.device != h.device:
+            raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    _check_tiles(tiles, block_m, h, "moe_gemm_down")
     _require_table(w_down, "w_down", n_experts, h)
     y = _out_buffer(out, n_rows, dim, h)
     if packed:
         _check(
             loader.library().astrai_moe_gemm_down_packed(
-                h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), sorted_w.data_ptr(), code, n_rows,
+                h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), _ptr(sorted_w), code, n_rows,
                 n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
             "moe_gemm_down_packed",
         )
         return y
     _check(
-        fn(h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), sorted_w.data_ptr(), code, n_rows,
+        fn(h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), _ptr(sorted_w), code, n_rows,
            n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
         "moe_gemm_down",
     )
@@ -346,35 +374,40 @@ def moe_combine(y: torch.Tensor, token_pos: torch.Tensor, shared: torch.Tensor |
     return out
 
 
-_dense_cache: dict[tuple, tuple[torch.Tensor, torch.Tensor]] = {}
-
-
-def _dense_tiles(n_tokens: int, block_m: int, device: torch.device, dtype: torch.dtype):
-    """Tile list and unit row weights for running one dense MLP over all
-    tokens (shared experts) through the grouped GEMMs."""
-    key = (n_tokens, block_m, device, dtype)
-    hit = _dense_cache.get(key)
-    if hit is None:
-        n = -(-n_tokens // block_m)
-        tl = [n, block_m, n, 0]
-        for i in range(n):
-            tl += [0, i * block_m, n_tokens]
-        hit = (torch.tensor(tl, dtype=torch.int32).to(device), torch.ones(n_tokens, dtype=dtype, device=device))
-        if len(_dense_cache) > 64:
-            _dense_cache.clear()
-        _dense_cache[key] = hit
-    return hit
+def dense_tiles(n_tokens: int, block_m: int, device: torch.device,
+                with_offsets: bool = False) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
+    """Tile list of one dense expert over ``n_tokens`` rows (the shared experts
+    and ``MLP``, mlp.py:22-25, on the grouped GEMMs), written on the device by
+    ``astrai_moe_dense_tiles``: a fresh allocation from torch's caching
+    allocator on every call, so a captured graph owns its list and no later
+    call can free or rewrite it. ``with_offsets`` also returns the expert
+    offsets ``{0, n_tokens}`` (int32[2]) the weight-gradient GEMM takes."""
+    tl = tile_list_len(n_tokens, 1, 1, block_m)
+    tiles = torch.empty(tl, dtype=torch.int32, device=device)
+    offsets = torch.empty(2, dtype=torch.int32, device=device) if with_offsets else None
+    _check(loader.library().astrai_moe_dense_tiles(n_tokens, block_m, tiles.data_ptr(), tl, _ptr(offsets),
+                                                   torch.cuda.current_stream(device).cuda_stream), "moe_dense_tiles")
+    _tag_tiles(tiles, block_m)
+    return (tiles, offsets) if with_offsets else tiles
 
 
 def moe_dense_mlp(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
-                  dim_ffn: int, out: torch.Tensor | None = None) -> torch.Tensor:
+                  dim_ffn: int, out: torch.Tensor | None = None, tiles: torch.Tensor | None = None) -> torch.Tensor:
     """One expert ``down(up(x) * silu(gate(x)))`` over all rows of x (mlp.py:22-25),
-    on the grouped-GEMM kernels with one-entry weight tables."""
+    on the grouped-GEMM kernels with one-entry weight tables. ``tiles``: a list
+    from ``dense_tiles`` for these rows at ``dense_block_m``'s height (built here
+    when None), so several experts over the same rows can share one."""
     n_tokens, dim = x.shape
-    block_m = select_block_m(n_tokens, 1, 1, dim, dim_ffn, x.dtype)
-    tiles, ones = _dense_tiles(n_tokens, block_m, x.device, x.dtype)
+    block_m = dense_block_m(n_tokens, dim, dim_ffn, x.dtype)
+    if tiles is None:
+        tiles = dense_tiles(n_tokens, block_m, x.device)
     h = moe_gemm_gate_up(x, tiles, w_gate, w_up, 1, dim_ffn, block_m)
-    return moe_gemm_down(h, tiles, w_down, ones, 1, dim, block_m, out=out)
+    return moe_gemm_down(h, tiles, w_down, None, 1, dim, block_m, out=out)
+
+
+def dense_block_m(n_tokens: int, dim: int, dim_ffn: int, dtype: torch.dtype) -> int:
+    """Row-tile height of one dense expert over ``n_tokens`` rows."""
+    return select_block_m(n_tokens, 1, 1, dim, dim_ffn, dtype)
 
 
 def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
@@ -424,6 +457,7 @@ def moe_gemm_gate_up_train(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: to
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
+    _check_tiles(tiles, TRAIN_BLOCK_M, x_perm, "moe_gemm_gate_up_train")
     _require_table(w_gate, "w_gate", n_experts, x_perm)
     _require_table(w_up, "w_up", n_experts, x_perm)
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
@@ -449,6 +483,7 @@ def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tens
     n_rows, dim_ffn = h.shape
     if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
         raise ValueError("sorted_w must hold one weight of h's dtype per row")
+    _check_tiles(tiles, TRAIN_BLOCK_M, h, "moe_gemm_down_train")
     _require_table(w_down, "w_down", n_experts, h)
     y, y_unw = (torch.empty(n_rows, dim, dtype=h.dtype, device=h.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_down_train", h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
@@ -481,6 +516,7 @@ def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Ten
     code = _dtype_code(dy, "dy")
     n_rows, dim = dy.shape
     dim_ffn = gu.shape[1] // 2
+    _check_tiles(tiles, TRAIN_BLOCK_M, dy, "moe_gemm_dgrad_down")
     _require_table(w_down, "w_down", n_experts, dy)
     dg, du = (torch.empty(n_rows, dim_ffn, dtype=dy.dtype, device=dy.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_dgrad_down", dy.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
@@ -495,6 +531,7 @@ def moe_gemm_dgrad_gate_up(dg: torch.Tensor, du: torch.Tensor, tiles: torch.Tens
     _require_gpu(dg, "dg", 2)
     code = _dtype_code(dg, "dg")
     n_rows, dim_ffn = dg.shape
+    _check_tiles(tiles, TRAIN_BLOCK_M, dg, "moe_gemm_dgrad_gate_up")
     _require_table(w_gate, "w_gate", n_experts, dg)
     _require_table(w_up, "w_up", n_experts, dg)
     dx = torch.empty(n_rows, dim, dtype=dg.dtype, device=dg.device)

@@ -140,6 +140,7 @@ class RoutedExperts(torch.autograd.Function):
     @staticmethod
     def _backward_hip(ctx, dout):
         x_perm, sorted_token, sorted_w, token_pos, offsets, tiles, h, gu, y_unw, *_ = ctx.saved_tensors
+        ops._tag_tiles(tiles, ops.TRAIN_BLOCK_M)
         n_experts = ctx.n_experts
         tg, tu, td = ctx.tables
         dim = x_perm.shape[1]
@@ -175,11 +176,11 @@ class DenseExpert(torch.autograd.Function):
         n_tokens, dim = x.shape
         ctx.hip = n_tokens > 0 and ops.backward_supported(dim, dim_ffn, x.dtype)
         if ctx.hip:
-            tiles, ones = ops._dense_tiles(n_tokens, ops.TRAIN_BLOCK_M, x.device, x.dtype)
+            tiles, offsets = ops.dense_tiles(n_tokens, ops.TRAIN_BLOCK_M, x.device, with_offsets=True)
             h, gu = ops.moe_gemm_gate_up_train(x, tiles, tg, tu, 1, dim_ffn)
-            out = ops.moe_gemm_down(h, tiles, td, ones, 1, dim, ops.TRAIN_BLOCK_M)
+            out = ops.moe_gemm_down(h, tiles, td, None, 1, dim, ops.TRAIN_BLOCK_M)
             ctx.tables = tables
-            ctx.save_for_backward(x, tiles, h, gu, wg, wu, wd)
+            ctx.save_for_backward(x, tiles, offsets, h, gu, wg, wu, wd)
             return out
         ctx.save_for_backward(x, wg, wu, wd)
         return ops.moe_dense_mlp(x, tg, tu, td, dim_ffn)
@@ -188,12 +189,12 @@ class DenseExpert(torch.autograd.Function):
     def backward(ctx, dout):
         dout = dout.contiguous()
         if ctx.hip:
-            x, tiles, h, gu, *_ = ctx.saved_tensors
+            x, tiles, offsets, h, gu, *_ = ctx.saved_tensors
+            ops._tag_tiles(tiles, ops.TRAIN_BLOCK_M)  # saved tensors come back without the tag
             tg, tu, td = ctx.tables
-            n_tokens, dim = x.shape
+            dim = x.shape[1]
             dg, du = ops.moe_gemm_dgrad_down(dout, tiles, td, gu, 1)
             dx = ops.moe_gemm_dgrad_gate_up(dg, du, tiles, tg, tu, 1, dim) if ctx.needs_input_grad[0] else None
-            offsets = torch.tensor([0, n_tokens], dtype=torch.int32, device=x.device)
             gg = ops.moe_gemm_wgrad(dg, x, offsets, 1)[0]
             gu = ops.moe_gemm_wgrad(du, x, offsets, 1)[0]
             gd = ops.moe_gemm_wgrad(dout, h, offsets, 1)[0]

@@ -79,12 +79,21 @@ class MLP(nn.Module):
             _plain_linear(self.down, "MLP"),
         )
 
+    def _weight_tables(self, wg: Tensor, wu: Tensor, wd: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+        """One-entry device pointer tables of the three weights, rebuilt only
+        when a weight's storage moves (a pageable host-to-device copy each)."""
+        key = (wg.data_ptr(), wu.data_ptr(), wd.data_ptr())
+        if getattr(self, "_table_key", None) != key:
+            self._tables = tuple(ops.expert_weight_table([w], tuple(w.shape)) for w in (wg, wu, wd))
+            self._table_key = key
+        return self._tables
+
     def forward(self, x: Tensor) -> Tensor:
         wg, wu, wd = self.weights()
         _check_gpu_input(x, [wg, wu, wd], "MLP")
         lead, dim = x.shape[:-1], x.shape[-1]
         x2 = x.reshape(-1, dim).contiguous()
-        tables = tuple(ops.expert_weight_table([w], tuple(w.shape)) for w in (wg, wu, wd))
+        tables = self._weight_tables(wg, wu, wd)
         if _needs_grad(x2, [wg, wu, wd]):
             out = DenseExpert.apply(x2, tables, wg.shape[0], wg, wu, wd)
         else:
@@ -194,7 +203,9 @@ class DeepSeekMoE(nn.Module):
     # -- forward ----------------------------------------------------------------
     def forward(self, x: Tensor) -> Tensor:
         bsz, seq_len, dim = x.shape
-        x_flat = x.view(-1, dim)
+        # the reference's view (mlp.py:66), then a dense copy when the view is
+        # strided (e.g. a slice of a wider buffer): the kernels take dense rows
+        x_flat = x.view(-1, dim).contiguous()
         params = list(self.parameters())
         _check_gpu_input(x_flat, params, "DeepSeekMoE")
         if _needs_grad(x_flat, params):
@@ -212,8 +223,10 @@ class DeepSeekMoE(nn.Module):
         _, t_shared = self._weight_tables()
         dim_ffn = self.shared_experts[0].up.weight.shape[0]
         out = torch.empty(self.n_shared_experts, x.shape[0], x.shape[1], dtype=x.dtype, device=x.device)
+        # one tile list for every shared expert: they run over the same rows
+        tiles = ops.dense_tiles(x.shape[0], ops.dense_block_m(x.shape[0], x.shape[1], dim_ffn, x.dtype), x.device)
         for i, (tg, tu, td) in enumerate(t_shared):
-            ops.moe_dense_mlp(x, tg, tu, td, dim_ffn, out=out[i])
+            ops.moe_dense_mlp(x, tg, tu, td, dim_ffn, out=out[i], tiles=tiles)
         return out
 
     def _routed_forward(self, x: Tensor, shared: Tensor | None = None) -> Tensor:

@@ -15,7 +15,11 @@ Prints one JSON line:
   kernels_ms      average time of every stage
   cpu_baseline    the reference path (the oracle's torch restatement of
                   mlp.py:64-100) on the host CPU, on a bounded token sample of
-                  the same layer
+                  the same layer, with every host core the process may use
+  parity          the timed configuration's output, routing and permutation
+                  against the oracle on the same device (outside the timed
+                  region): routing and permutation bit-exact flags, the plain
+                  allclose pass fraction and the max normalised error
 """
 
 from __future__ import annotations
@@ -50,6 +54,7 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--workload", default=None, help="workload name (default: the Mixtral-shaped layer)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-parity", action="store_true", help="skip the parity check against the oracle")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU work for the baseline sample")
     p.add_argument("--backward", action="store_true",
                    help="also time forward + backward (reported as train_*; value stays the forward)")
@@ -104,11 +109,53 @@ class StageTimer:
         return {k: (sum(s.elapsed_time(e) for s, e in v) / len(v) if v else 0.0) for k, v in events.items()}
 
 
+def host_cores() -> tuple[int, dict]:
+    """Threads for the CPU baseline: every CPU in the process's affinity mask,
+    capped by the container's CPU quota and by the job's thread budget
+    (``OMP_NUM_THREADS``) when either is set — threads beyond the CPUs the job
+    is granted only time-slice. Returns (threads, the figures it came from)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = int(q) / int(period)
+    except (OSError, ValueError):
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS")
+    omp_n = int(omp) if omp and omp.isdigit() and int(omp) > 0 else None
+    cores = affinity
+    if quota is not None:
+        cores = min(cores, max(1, int(quota + 0.5)))
+    if omp_n is not None:
+        cores = min(cores, omp_n)
+    return cores, {"affinity_cpus": affinity, "cgroup_cpu_quota": quota, "omp_num_threads": omp_n}
+
+
+def parity_leg(layer, x, w, ops) -> dict:
+    """Checker leg, outside the timed region: the timed configuration's layer
+    output, the route kernel's expert sets and weights and the permutation's
+    row order and offsets against the oracle on the same device."""
+    from oracle import parity as P
+
+    with torch.inference_mode():
+        out = layer(x)
+        x_flat = x.view(-1, w.dim)
+        route = ops.moe_route(layer.router(x_flat), w.top_k)
+        block_m = ops.select_block_m(w.n_tokens, w.n_experts, w.top_k, w.dim, w.dim_ffn, w.dtype)
+        perm = ops.moe_permute(route, x_flat, w.n_experts, block_m, copy_rows=False)
+        rep = P.layer_parity(layer, x, out, route.topk_idx, route.topk_w, perm.sorted_token, perm.expert_offsets)
+    torch.cuda.synchronize()
+    return rep
+
+
 def cpu_baseline(layer, x, w, target_s: float) -> dict:
     """The reference path on the host CPU (bounded token sample)."""
     from oracle import moe_ref as R
 
-    threads = torch.get_num_threads()
+    threads, host = host_cores()
+    torch.set_num_threads(threads)
     rw, rb, experts, shared = R.module_weights(layer)
     to_cpu = lambda t: None if t is None else t.detach().cpu()  # noqa: E731
     rw, rb = to_cpu(rw), to_cpu(rb)
@@ -141,6 +188,7 @@ def cpu_baseline(layer, x, w, target_s: float) -> dict:
         "kind": "port",
         "sample": f"first {n} of {x_all.shape[0]} tokens{passes} of the same layer and inputs, reference torch "
                   f"path (mlp.py:79-100) on CPU in {str(w.dtype).replace('torch.', '')}, {dt:.1f} s",
+        **host,
     }
 
 
@@ -303,6 +351,8 @@ def main():
     if graph_ms is not None:
         result["graph_ms_per_step"] = graph_ms
         result["graph_value"] = T / (graph_ms / 1e3)
+    if not args.no_parity:
+        result["parity"] = parity_leg(layer, x, w, ops)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(layer, x, w, args.cpu_seconds)
     print(json.dumps(result), flush=True)

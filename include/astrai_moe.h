@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 4
+#define ASTRAI_MOE_ABI_VERSION 5
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -124,6 +124,21 @@ int astrai_moe_permute(const int32_t* topk_idx, const void* topk_w,
                        int64_t tiles_len, int32_t* chunk_base, void* stream);
 
 /*
+ * Tile list of one dense expert over n_rows rows: every row belongs to expert
+ * 0, in ceil(n_rows / block_m) row tiles (layout above), and, when
+ * expert_offsets is not NULL, its offsets {0, n_rows} (int32[2]). With
+ * one-entry weight tables and no row weights (sorted_w = NULL) the grouped
+ * GEMMs then compute mlp.py:22-25, MLP.forward, over all rows: the shared
+ * experts of mlp.py:74-77 and the standalone MLP. Written on the device, so a
+ * caller that captures its forward in a graph captures the list with it.
+ *
+ *   tiles  astrai_moe_tile_list_len(n_rows, 1, 1, block_m) int32
+ */
+int astrai_moe_dense_tiles(int64_t n_rows, int block_m, int32_t* tiles,
+                           int64_t tiles_len, int32_t* expert_offsets,
+                           void* stream);
+
+/*
  * Grouped gate/up projection with fused SwiGLU.
  * Replaces mlp.py:22-23 (up(x) * silu(gate(x))) for every expert at once,
  * rounding to dtype where the reference does: after gate, after up, after
@@ -165,7 +180,8 @@ int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token,
  *
  *   h         [n_rows, dim_ffn]   dtype
  *   w_down    device array of n_experts pointers, each [dim, dim_ffn]
- *   sorted_w  [n_rows]            dtype, from astrai_moe_permute
+ *   sorted_w  [n_rows]            dtype, from astrai_moe_permute; NULL for
+ *                                 weight 1 (a dense expert: mlp.py:22-25)
  *   y         [n_rows, dim]       dtype
  */
 int astrai_moe_gemm_down(const void* h, const int32_t* tiles,

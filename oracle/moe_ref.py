@@ -1,9 +1,10 @@
 """ORACLE — test infrastructure only. Restatement of AstrAI's MoE forward.
 
-Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
-leg may import this module, and only as the checker (or, for the CPU
-baseline, as the reference path being timed). The product path
-(``astrai_amd``) never imports it.
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s checker legs
+(the CPU baseline and the parity report, through ``oracle/parity.py``) may
+import this module, and only as the checker (or, for the CPU baseline, as the
+reference path being timed). The product path (``astrai_amd``) never imports
+it.
 
 What it restates: ``astrai/model/components/mlp.py:14-25`` (MLP) and
 ``:64-100`` (DeepSeekMoE.forward / _shared_forward / _routed_forward), with

@@ -1,10 +1,13 @@
 """HIP-graph capture of the layer forward (serving loops replay captured
 decode steps). The whole forward — router GEMM, route, permute, grouped GEMMs,
-combine — is captured on one stream after a warm-up call (which builds the
-weight-pointer tables), then replayed several times with eager work in
-between; every replay must equal the eager result bit for bit, and a replay
-after the input buffer is refilled must equal the eager result on the new
-input.
+combine, and the shared experts' dense tile list — is captured on one stream
+after a warm-up call (which builds the weight-pointer tables), then replayed
+several times with eager work in between. Every replay must equal the eager
+result bit for bit, and must match the oracle (the reference's torch forward,
+mlp.py:64-100, on the same device): bit-exact routing, and the layer
+tolerance per expert term plus >= 99.9 % plain allclose. A replay after the
+input buffer is refilled must equal the eager result on the new input and
+match the oracle on it.
 """
 
 from __future__ import annotations
@@ -12,8 +15,10 @@ from __future__ import annotations
 import pytest
 import torch
 
+from astrai_amd.extension import ops
 from astrai_amd.model.components.mlp import DeepSeekMoE
 from astrai_amd.workloads import WORKLOADS, make_layer
+from oracle import parity as P
 
 pytestmark = pytest.mark.gpu
 
@@ -27,32 +32,50 @@ def _layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype):
     return layer.to(device=gpu, dtype=dtype).requires_grad_(False)
 
 
+def _assert_oracle(layer, x, out, label):
+    logits = layer.router(x.view(-1, x.shape[-1]))
+    res = ops.moe_route(logits, layer.n_activated_experts)
+    rep = P.layer_parity(layer, x, out, res.topk_idx, res.topk_w)
+    torch.cuda.synchronize()
+    print(f"{label}: allclose={rep['allclose_frac']:.6f} worst(err-bound)={rep['term_bound_excess']:.3e}")
+    assert rep["routing_bit_exact"], f"{label}: routing differs from the reference"
+    assert rep["term_bound_excess"] <= 0, f"{label}: error exceeds the per-term tolerance"
+    assert rep["allclose_frac"] >= 0.999, f"{label}: allclose pass fraction {rep['allclose_frac']}"
+
+
+def _capture(layer, static_x):
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        layer(static_x)  # warm-up on the capture stream
+        stream.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            static_out = layer(static_x)
+    torch.cuda.current_stream().wait_stream(stream)
+    return graph, static_out
+
+
 def _check_graph(layer, x):
     static_x = x.clone()
     with torch.inference_mode():
         eager = layer(static_x)
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        stream = torch.cuda.Stream()
-        stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
-            layer(static_x)  # warm-up on the capture stream
-            stream.synchronize()
-            with torch.cuda.graph(graph, stream=stream):
-                static_out = layer(static_x)
-        torch.cuda.current_stream().wait_stream(stream)
+        graph, static_out = _capture(layer, static_x)
         for i in range(4):
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(static_out, eager), f"replay {i} differs from the eager forward"
             noise = torch.randn(1024, 1024, device=x.device) @ torch.randn(1024, 1024, device=x.device)
             del noise
+        _assert_oracle(layer, static_x, static_out, "replay")
         x2 = torch.randn_like(x.float()).to(x.dtype)
         eager2 = layer(x2)
         static_x.copy_(x2)
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(static_out, eager2), "replay on a refilled input differs from the eager forward"
+        _assert_oracle(layer, static_x, static_out, "replay on a refilled input")
 
 
 def test_graph_decode_workload(gpu):
@@ -76,3 +99,26 @@ def test_graph_packed_weights(gpu):
     layer.pack_weights = True
     x = torch.randn(1, 200, 512, device=gpu).to(torch.bfloat16)
     _check_graph(layer, x)
+
+
+def test_graph_survives_many_eager_token_counts(gpu):
+    # a serving loop: decode steps replayed from a graph, eager prefills of
+    # many different lengths in between. Everything the captured forward reads
+    # (the shared experts' tile list included) must belong to the graph, so the
+    # eager calls cannot free or rewrite it.
+    layer = _layer(gpu, 256, 512, 8, 2, 2, torch.bfloat16)
+    static_x = torch.randn(1, 48, 256, device=gpu).to(torch.bfloat16)
+    with torch.inference_mode():
+        eager = layer(static_x)
+        graph, static_out = _capture(layer, static_x)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager)
+        for n in range(1, 141, 2):  # 70 distinct token counts
+            layer(torch.randn(1, n, 256, device=gpu).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        for i in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(static_out, eager), f"replay {i} after the eager calls differs"
+        _assert_oracle(layer, static_x, static_out, "replay after 70 eager token counts")

@@ -389,3 +389,39 @@ def test_combine_bit_exact(gpu, n_tok, n_exp, top_k, dim, n_shared, dtype):
     ref = sh + ref
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("n_tok,dim,dim_ffn,dtype", [
+    (1, 256, 128, torch.bfloat16),      # 32-row tiles
+    (200, 256, 256, torch.bfloat16),    # 64-row tiles
+    (3000, 2048, 2048, torch.bfloat16), # 256-row tiles
+    (37, 40, 24, torch.bfloat16),       # general kernel
+    (129, 64, 96, torch.float32),       # general kernel, fp32
+])
+def test_dense_expert_tile_list_and_gemms(gpu, n_tok, dim, dim_ffn, dtype):
+    # one dense expert (the shared experts, MLP; mlp.py:22-25) over all rows:
+    # the device-built tile list has the layout the permutation writes, and the
+    # down GEMM without row weights multiplies by nothing
+    bm = ops.dense_block_m(n_tok, dim, dim_ffn, dtype)
+    tiles, offsets = ops.dense_tiles(n_tok, bm, gpu, with_offsets=True)
+    n = -(-n_tok // bm)
+    want = [n, bm, n, 0] + [v for i in range(n) for v in (0, i * bm, n_tok)]
+    torch.cuda.synchronize()
+    assert tiles.tolist() == want and offsets.tolist() == [0, n_tok]
+    g = torch.Generator(device=gpu).manual_seed(5)
+    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    w = R.ExpertWeights(*(torch.randn(s, generator=g, device=gpu).mul(0.05).to(dtype)
+                          for s in ((dim_ffn, dim), (dim_ffn, dim), (dim, dim_ffn))))
+    tg, tu, td = (ops.expert_weight_table([t], tuple(t.shape)) for t in (w.gate, w.up, w.down))
+    out = ops.moe_dense_mlp(x, tg, tu, td, dim_ffn, tiles=tiles)
+    h = ops.moe_gemm_gate_up(x, tiles, tg, tu, 1, dim_ffn, bm)
+    ones = torch.ones(n_tok, dtype=dtype, device=gpu)
+    y_ones = ops.moe_gemm_down(h, tiles, td, ones, 1, dim, bm)
+    tol = BF16_TOL if dtype == torch.bfloat16 else FP32_TOL
+    torch.cuda.synchronize()
+    assert torch.equal(out, y_ones)  # no row weights == weight 1, bit for bit
+    # each GEMM against torch on the same inputs, at the reference's rounding points
+    torch.testing.assert_close(h, F.linear(x, w.up) * F.silu(F.linear(x, w.gate)), **tol)  # mlp.py:23
+    torch.testing.assert_close(out, F.linear(h, w.down), **tol)  # mlp.py:24
+    with pytest.raises(ValueError, match="built for block_m"):
+        ops.moe_gemm_gate_up(x, tiles, tg, tu, 1, dim_ffn, 256 if bm != 256 else 64)

@@ -336,3 +336,41 @@ def test_weight_tables_are_checked_before_any_launch(monkeypatch):
                     continue  # an argument this wrapper does not read
                 with pytest.raises(ValueError, match=r"^w_(gate|up|down)"):
                     call(*args)
+
+
+def test_tile_list_height_is_checked_before_any_launch(monkeypatch):
+    # a tile list of one height run with another would compute only part of
+    # each tile and leave the rest of the output unwritten: the wrappers
+    # compare the height a list was built for with their block_m
+    def relaxed(t, name, ndim=None):
+        if not isinstance(t, torch.Tensor) or not t.is_contiguous() or (ndim is not None and t.dim() != ndim):
+            raise ValueError(name)
+
+    monkeypatch.setattr(ops, "_require_gpu", relaxed)
+    monkeypatch.setattr(ops, "_kernel", lambda name: lambda *args: _NoLaunch().__getattr__(name))
+    monkeypatch.setattr(ops, "loader", _NoLaunch())
+    monkeypatch.setattr(ops, "_stream", lambda t: 0)
+    n_exp, dim, dim_ffn, bf = 4, 256, 128, torch.bfloat16
+    x = torch.zeros(64, dim, dtype=bf)
+    good = torch.zeros(n_exp, dtype=torch.int64)
+    for built in (32, 64, 256):
+        tiles = ops._tag_tiles(torch.zeros(64, dtype=torch.int32), built)
+        for name, call in _table_wrappers(x, tiles, n_exp, dim, dim_ffn).items():
+            runs_at = 256 if name.endswith("train") or name.startswith("dgrad") else 32
+            if built == runs_at:
+                with pytest.raises(AssertionError, match="reached the library"):
+                    call(good, good, good)
+            else:
+                with pytest.raises(ValueError, match=f"built for block_m {built}"):
+                    call(good, good, good)
+    # and a tile list must be an int32 list
+    with pytest.raises(ValueError, match="int32 tile list"):
+        ops.moe_gemm_gate_up(x, torch.zeros(64, dtype=torch.int64), good, good, n_exp, dim_ffn, 32)
+
+
+def test_dense_tile_lists_are_not_cached_across_calls():
+    # a graph captured with a dense expert must own its tile list: the ops
+    # build one per call on the device instead of keeping a module-level cache
+    # that later calls could clear and the allocator reuse
+    assert not any("cache" in name for name in vars(ops) if name.startswith("_dense"))
+    assert "astrai_moe_dense_tiles" in loader._SIGNATURES

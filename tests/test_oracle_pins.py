@@ -321,3 +321,51 @@ def test_combine_order_mistake_is_caught(monkeypatch):
     monkeypatch.setattr(R, "routed_forward", orig)
     got = R.routed_forward(x, rw, None, experts, 3).double().numpy()
     assert np.mean(got == ref) >= 0.99
+
+
+# -- the parity checker (oracle/parity.py) ---------------------------------------
+
+
+def _cpu_layer(dtype, n_shared=1, top_k=2):
+    from astrai_amd.model.components.mlp import DeepSeekMoE
+
+    torch.manual_seed(11)
+    layer = DeepSeekMoE(32, 48, 6, n_shared_experts=n_shared, n_activated_experts=top_k)
+    for m in layer.modules():
+        if hasattr(m, "reset_parameters"):
+            m.reset_parameters()
+    return layer.to(dtype).requires_grad_(False)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_parity_checker_passes_the_reference_and_catches_mistakes(dtype):
+    from oracle import parity as P
+
+    layer = _cpu_layer(dtype)
+    x = torch.randn(2, 40, 32).to(dtype)
+    ref = R.module_forward(layer, x)
+    logits = layer.router(x.view(-1, 32))
+    w, idx = R.route(logits, 2, dtype)
+    tok, _, offsets = R.permutation(idx, 6)
+    rep = P.layer_parity(layer, x, ref, idx.int(), w, tok.int(), offsets.int())
+    assert rep["allclose_frac"] == 1.0 and rep["max_norm_err"] == 0.0 and rep["term_bound_excess"] < 0
+    assert rep["routing_bit_exact"] and rep["permutation_bit_exact"] and rep["finite"]
+    # slot order of the ids does not matter (sets), the weights must match slot by slot
+    assert P.layer_parity(layer, x, ref, idx.flip(-1).int(), w)["routing_bit_exact"]
+    assert not P.layer_parity(layer, x, ref, idx.int(), w.flip(-1))["routing_bit_exact"] or torch.equal(w, w.flip(-1))
+    # planted mistakes: one wrong output element, a wrong expert, a swapped permuted row, a wrong offset
+    bad = ref.clone()
+    bad.view(-1)[7] += 0.25
+    rb = P.layer_parity(layer, x, bad)
+    assert rb["allclose_frac"] < 1.0 and rb["max_norm_err"] > 1.0 and rb["term_bound_excess"] > 0
+    idx_bad = idx.clone()
+    idx_bad[3, 0] = (idx_bad[3, 0] + 1) % 6 if (idx_bad[3, 0] + 1) % 6 != idx_bad[3, 1] else (idx_bad[3, 0] + 2) % 6
+    assert not P.layer_parity(layer, x, ref, idx_bad.int(), w)["routing_bit_exact"]
+    tok_bad = tok.clone()
+    tok_bad[[0, 1]] = tok_bad[[1, 0]]
+    assert not P.layer_parity(layer, x, ref, sorted_token=tok_bad.int(), expert_offsets=offsets.int())[
+        "permutation_bit_exact"]
+    off_bad = offsets.clone()
+    off_bad[2] += 1
+    assert not P.layer_parity(layer, x, ref, sorted_token=tok.int(), expert_offsets=off_bad.int())[
+        "permutation_bit_exact"]
