@@ -6,15 +6,25 @@
 // row order is the concatenation over experts, so it is fixed exactly:
 // expert-major, token-ascending. Integer work only; results are bit-exact.
 //
-// Two kernels:
-//   scan_kernel     one block. Column sums of the per-chunk histograms give
-//                   per-expert counts; a block-wide exclusive scan (wave64
-//                   shuffle scan + LDS for wave totals) gives expert offsets;
-//                   per-chunk bases give every chunk its first slot in each
-//                   expert's segment; the GEMM row-tile list is laid out from
-//                   the counts (tiles never straddle experts, empty experts
-//                   get none) so no host synchronisation is needed.
-//   scatter_kernel  grid (chunk, column split). Wave 0 ranks the chunk's
+// Kernels:
+//   range_sum_kernel  (many chunks; see kScanDirectRows) one block per range
+//                   of kRangeChunks token chunks: the range's per-expert
+//                   counts, the column sums of its chunk histograms.
+//   scan_kernel     one block, over the ranges (or, for few chunks, over the
+//                   chunks themselves). Column sums give per-expert counts; a
+//                   block-wide exclusive scan (wave64 shuffle scan + LDS for
+//                   wave totals) gives expert offsets (the split partial sums
+//                   of each expert column are scanned by wave shuffles, not
+//                   walked by one thread); per-range bases give
+//                   every range its first slot in each expert's segment; the
+//                   GEMM row-tile list is laid out from the counts (tiles
+//                   never straddle experts, empty experts get none) so no
+//                   host synchronisation is needed. Splitting the column sums
+//                   off into many blocks keeps the one-block part short: it
+//                   walks n_chunks / kRangeChunks rows instead of n_chunks.
+//   scatter_kernel  grid (chunk, column split). A chunk's first slot in each
+//                   expert's segment is its range's base plus the histograms
+//                   of the earlier chunks of its range. Wave 0 ranks the chunk's
 //                   (token, slot) entries in order: lanes holding the same
 //                   expert are found with one ballot per expert-id bit, the
 //                   rank is the popcount of lower peer lanes, and an LDS
@@ -31,6 +41,28 @@ namespace {
 
 constexpr int kScanThreads = 1024;
 constexpr int kScatterThreads = 256;
+// Token chunks per scan range. The scan walks the chunks directly (one
+// launch) while each of its threads has at most kScanDirectRows chunks to
+// walk, and ranges of kRangeChunks chunks beyond that.
+constexpr int kRangeChunks = 8;
+constexpr int kScanDirectRows = 32;
+
+// Per-expert counts of each range of kRangeChunks chunks:
+// range_sum[r, e] = sum over the range's chunks c of chunk_hist[c, e].
+__global__ __launch_bounds__(256) void range_sum_kernel(
+    const int32_t* __restrict__ chunk_hist, int64_t n_chunks_, int n_experts,
+    int32_t* __restrict__ range_sum) {
+  const int64_t r = blockIdx.x;
+  const int64_t c0 = r * kRangeChunks;
+  const int64_t c1 = min(c0 + (int64_t)kRangeChunks, n_chunks_);
+  for (int e = threadIdx.x; e < n_experts; e += 256) {
+    int v = 0;
+#pragma unroll
+    for (int i = 0; i < kRangeChunks; ++i)
+      if (c0 + i < c1) v += chunk_hist[(c0 + i) * n_experts + e];
+    range_sum[r * n_experts + e] = v;
+  }
+}
 
 // Inclusive scan of `v` over the block (blockDim.x == kScanThreads).
 __device__ int block_inclusive_scan(int v, int* s_wave) {
@@ -58,50 +90,78 @@ __device__ int block_inclusive_scan(int v, int* s_wave) {
   return r;
 }
 
+// Over `n_rows_` rows of per-expert counts (ranges or chunks): expert offsets,
+// the tile list and each row's base (expert offset + counts of the earlier
+// rows). `base` may alias `hist`: every element is read before it is written,
+// by the same thread.
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
-    const int32_t* __restrict__ chunk_hist, int64_t n_chunks_, int n_experts,
+    const int32_t* hist, int64_t n_rows_, int n_experts,
     int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
-    int32_t* __restrict__ chunk_base, int32_t* __restrict__ tiles) {
+    int32_t* base, int32_t* __restrict__ tiles) {
   __shared__ int s_part[kScanThreads];
   __shared__ int s_wave[kScanThreads / 64];
+  __shared__ int s_cnt[ASTRAI_MOE_MAX_EXPERTS];
   __shared__ int s_off[ASTRAI_MOE_MAX_EXPERTS];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
 
   // Threads form a [splits][ep] grid: ep = next_pow2(E) expert columns, each
-  // column's chunks split into `splits` contiguous ranges.
+  // column's rows split into `splits` contiguous runs.
   int ep = 1;
   while (ep < n_experts) ep *= 2;
   const int splits = kScanThreads / ep;
   const int e = threadIdx.x % ep;
   const int s = threadIdx.x / ep;
-  const int64_t per = ceil_div(n_chunks_, splits);
-  const int64_t c0 = min((int64_t)s * per, n_chunks_);
-  const int64_t c1 = min(c0 + per, n_chunks_);
+  const int64_t per = ceil_div(n_rows_, splits);
+  const int64_t c0 = min((int64_t)s * per, n_rows_);
+  const int64_t c1 = min(c0 + per, n_rows_);
 
   int local = 0;
-  if (e < n_experts)
-    for (int64_t c = c0; c < c1; ++c) local += chunk_hist[c * n_experts + e];
+  if (e < n_experts) {
+#pragma unroll 8
+    for (int64_t c = c0; c < c1; ++c) local += hist[c * n_experts + e];
+  }
   s_part[threadIdx.x] = local;
   __syncthreads();
-  // Exclusive prefix over the splits of each expert column.
-  if (s == 0) {
-    int run = 0;
-    for (int j = 0; j < splits; ++j) {
-      const int v = s_part[j * ep + e];
-      s_part[j * ep + e] = run;
-      run += v;
+
+  // Exclusive prefix over the splits of each expert column, in parallel: one
+  // wave per group of columns, lane l holding split (l % sl) of column
+  // (l / sl) of its group; columns with more than 64 splits take several
+  // passes with a carry. The column's total is its expert's count.
+  {
+    const int sl = splits < 64 ? splits : 64;
+    const int cpw = 64 / sl;  // columns per wave
+    if (wave < ep / cpw) {
+      const int col = wave * cpw + lane / sl;
+      const int j0 = lane % sl;
+      const int seg_last = (lane / sl) * sl + sl - 1;
+      int carry = 0;
+      for (int jb = 0; jb < splits; jb += sl) {
+        const int j = jb + j0;
+        const int v = s_part[j * ep + col];
+        int incl = v;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int o = __shfl_up(incl, off, 64);
+          if (off < sl && j0 >= off) incl += o;
+        }
+        s_part[j * ep + col] = carry + incl - v;
+        carry += __shfl(incl, seg_last, 64);
+      }
+      if (j0 == sl - 1 && col < n_experts) s_cnt[col] = carry;
     }
-    s_off[e] = e < n_experts ? run : 0;
   }
   __syncthreads();
 
   // Expert offsets and tile starts: block scans over expert ids.
-  const int cnt = (threadIdx.x < n_experts) ? s_off[threadIdx.x] : 0;
+  const int cnt = (threadIdx.x < n_experts) ? s_cnt[threadIdx.x] : 0;
   const int ntile = (cnt + block_m - 1) / block_m;
   const int cnt_incl = block_inclusive_scan(cnt, s_wave);
   const int tile_incl = block_inclusive_scan(ntile, s_wave);
-  const int off = cnt_incl - cnt;
-  const int tile0 = tile_incl - ntile;
   if (threadIdx.x < n_experts) {
+    const int off = cnt_incl - cnt;
+    const int tile0 = tile_incl - ntile;
+    s_off[threadIdx.x] = off;
     expert_offsets[threadIdx.x] = off;
     if (threadIdx.x == n_experts - 1) {
       expert_offsets[n_experts] = cnt_incl;
@@ -110,24 +170,23 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       tiles[2] = (int32_t)tile_capacity;
       tiles[3] = 0;
     }
+    // the expert's row tiles (stores only: nothing waits on them)
     for (int j = 0; j < ntile && tile0 + j < tile_capacity; ++j) {
-      int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER +
-                   (int64_t)(tile0 + j) * ASTRAI_MOE_TILE_STRIDE;
+      int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)(tile0 + j) * ASTRAI_MOE_TILE_STRIDE;
       t[0] = threadIdx.x;
       t[1] = off + j * block_m;
       t[2] = off + cnt;
     }
   }
   __syncthreads();
-  if (threadIdx.x < n_experts) s_off[threadIdx.x] = off;
-  __syncthreads();
 
-  // Chunk bases: expert offset + tokens of that expert in earlier chunks.
+  // Row bases: expert offset + tokens of that expert in earlier rows.
   if (e < n_experts) {
     int run = s_off[e] + s_part[threadIdx.x];
+#pragma unroll 8
     for (int64_t c = c0; c < c1; ++c) {
-      const int v = chunk_hist[c * n_experts + e];
-      chunk_base[c * n_experts + e] = run;
+      const int v = hist[c * n_experts + e];
+      base[c * n_experts + e] = run;
       run += v;
     }
   }
@@ -136,7 +195,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 template <typename T, bool kVec>
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     const int32_t* __restrict__ topk_idx, const T* __restrict__ topk_w,
-    const int32_t* __restrict__ chunk_base, const T* __restrict__ x,
+    const int32_t* __restrict__ chunk_hist, const int32_t* __restrict__ range_base,
+    int range_chunks, const T* __restrict__ x,
     int64_t n_tokens, int n_experts, int top_k, int64_t dim,
     int32_t* __restrict__ sorted_token, T* __restrict__ sorted_w,
     int32_t* __restrict__ token_pos, T* __restrict__ x_perm) {
@@ -148,8 +208,16 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   const int nt = (int)min((int64_t)ASTRAI_MOE_CHUNK_TOKENS, n_tokens - t0);
   const int n_ent = nt * top_k;
   const int64_t n_rows = n_tokens * top_k;
-  for (int e = threadIdx.x; e < n_experts; e += kScatterThreads)
-    cnt[e] = chunk_base[chunk * n_experts + e];
+  {
+    // the chunk's first slot per expert: its range's base plus the earlier
+    // chunks of the range
+    const int64_t r = chunk / range_chunks;
+    for (int e = threadIdx.x; e < n_experts; e += kScatterThreads) {
+      int b = range_base[r * n_experts + e];
+      for (int64_t c = r * range_chunks; c < chunk; ++c) b += chunk_hist[c * n_experts + e];
+      cnt[e] = b;
+    }
+  }
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
@@ -257,10 +325,25 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
                    int32_t* tiles, int64_t tile_capacity, int32_t* chunk_base,
                    hipStream_t s) {
   const int64_t nc = n_chunks(n_tokens);
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s, chunk_hist,
-                     nc, n_experts, block_m, tile_capacity, expert_offsets,
-                     chunk_base, tiles);
-  int rc = check_launch("scan_kernel");
+  // the scan's rows: ranges of kRangeChunks chunks (their counts summed into
+  // the scratch first, then scanned in place), or the chunks themselves
+  int ep = 1;
+  while (ep < n_experts) ep *= 2;
+  const int64_t rows_per_thread = ceil_div(nc, kScanThreads / ep);
+  const int range_chunks = rows_per_thread > kScanDirectRows ? kRangeChunks : 1;
+  const int64_t n_ranges = ceil_div(nc, range_chunks);
+  int32_t* range_base = chunk_base;  // n_ranges * n_experts <= n_chunks * n_experts
+  int rc = ASTRAI_MOE_OK;
+  if (range_chunks > 1) {
+    hipLaunchKernelGGL(range_sum_kernel, dim3((unsigned)n_ranges), dim3(256), 0, s,
+                       chunk_hist, nc, n_experts, range_base);
+    if ((rc = check_launch("range_sum_kernel"))) return rc;
+  }
+  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s,
+                     range_chunks > 1 ? range_base : chunk_hist, n_ranges,
+                     n_experts, block_m, tile_capacity, expert_offsets,
+                     range_base, tiles);
+  rc = check_launch("scan_kernel");
   if (rc || nc == 0) return rc;
   const bool vec = (dim * (int64_t)sizeof(T)) % 16 == 0 &&
                    (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
@@ -275,15 +358,17 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
   if (vec)
     hipLaunchKernelGGL((scatter_kernel<T, true>), grid,
                        dim3(kScatterThreads), 0, s, topk_idx,
-                       static_cast<const T*>(topk_w), chunk_base,
-                       static_cast<const T*>(x), n_tokens, n_experts, top_k,
+                       static_cast<const T*>(topk_w), chunk_hist, range_base,
+                       range_chunks, static_cast<const T*>(x), n_tokens,
+                       n_experts, top_k,
                        dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
                        static_cast<T*>(x_perm));
   else
     hipLaunchKernelGGL((scatter_kernel<T, false>), grid,
                        dim3(kScatterThreads), 0, s, topk_idx,
-                       static_cast<const T*>(topk_w), chunk_base,
-                       static_cast<const T*>(x), n_tokens, n_experts, top_k,
+                       static_cast<const T*>(topk_w), chunk_hist, range_base,
+                       range_chunks, static_cast<const T*>(x), n_tokens,
+                       n_experts, top_k,
                        dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
                        static_cast<T*>(x_perm));
   return check_launch("scatter_kernel");
