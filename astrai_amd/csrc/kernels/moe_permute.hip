@@ -34,6 +34,8 @@
 //                   top_k destinations with 16-byte vector accesses. Column
 //                   splits keep enough workgroups in flight when there are
 //                   few tokens (decode).
+#include <mutex>
+
 #include "moe_common.h"
 
 namespace astrai_moe {
@@ -316,6 +318,22 @@ __global__ __launch_bounds__(256) void dense_tiles_kernel(
   }
 }
 
+// Chunks per row of the scan: ranges of kRangeChunks chunks (their counts
+// summed into the scratch first, then scanned in place) when each scan thread
+// would otherwise walk more than kScanDirectRows chunks, else the chunks.
+int scan_range_chunks(int64_t n_tokens, int n_experts) {
+  int ep = 1;
+  while (ep < n_experts) ep *= 2;
+  const int64_t rows_per_thread = ceil_div(n_chunks(n_tokens), kScanThreads / ep);
+  return rows_per_thread > kScanDirectRows ? kRangeChunks : 1;
+}
+
+// int32 elements of scratch the permutation uses: one row of expert bases per
+// scan row (at most n_chunks * n_experts).
+int64_t permute_scratch_ints(int64_t n_tokens, int n_experts) {
+  return ceil_div(n_chunks(n_tokens), scan_range_chunks(n_tokens, n_experts)) * n_experts;
+}
+
 template <typename T>
 int launch_permute(const int32_t* topk_idx, const void* topk_w,
                    const int32_t* chunk_hist, const void* x, int64_t n_tokens,
@@ -325,12 +343,7 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
                    int32_t* tiles, int64_t tile_capacity, int32_t* chunk_base,
                    hipStream_t s) {
   const int64_t nc = n_chunks(n_tokens);
-  // the scan's rows: ranges of kRangeChunks chunks (their counts summed into
-  // the scratch first, then scanned in place), or the chunks themselves
-  int ep = 1;
-  while (ep < n_experts) ep *= 2;
-  const int64_t rows_per_thread = ceil_div(nc, kScanThreads / ep);
-  const int range_chunks = rows_per_thread > kScanDirectRows ? kRangeChunks : 1;
+  const int range_chunks = scan_range_chunks(n_tokens, n_experts);
   const int64_t n_ranges = ceil_div(nc, range_chunks);
   int32_t* range_base = chunk_base;  // n_ranges * n_experts <= n_chunks * n_experts
   int rc = ASTRAI_MOE_OK;
@@ -388,32 +401,82 @@ extern "C" int64_t astrai_moe_tile_list_len(int64_t n_tokens, int n_experts,
   return ASTRAI_MOE_TILE_HEADER + cap * ASTRAI_MOE_TILE_STRIDE;
 }
 
-extern "C" int astrai_moe_permute(
+// Scratch of astrai_moe_permute_noalloc: the scan's per-row expert bases
+// (permute_scratch_ints) live here instead of in a caller-provided buffer.
+// Every GPU the library runs on holds its own copy until the process ends.
+// Nothing in it has to start at zero: the scan writes every element it later
+// reads. Calls that overlap on one GPU (two streams, two host threads) share
+// it and race.
+static __device__ __align__(256) int32_t scratch[ASTRAI_MOE_NOALLOC_SCRATCH_INTS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device. In host code the
+// array's name is a host-side stand-in, never a device address: the address
+// comes from hipGetSymbolAddress, once per device with that device current,
+// and is used wherever host code needs the array (kernel arguments).
+int noalloc_scratch(int32_t** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(ASTRAI_MOE_ELAUNCH, "permute_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(ASTRAI_MOE_EINVAL, "permute_noalloc: device %d beyond the %d this build tracks", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr)
+      return fail(ASTRAI_MOE_ELAUNCH, "permute_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(err));
+    g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return ASTRAI_MOE_OK;
+}
+}  // namespace
+
+static int permute_impl(const char* who,
     const int32_t* topk_idx, const void* topk_w, const int32_t* chunk_hist,
     const void* x, int dtype, int64_t n_tokens, int n_experts, int top_k,
     int64_t dim, int block_m, int32_t* expert_offsets, int32_t* sorted_token,
     void* sorted_w, int32_t* token_pos, void* x_perm, int32_t* tiles,
-    int64_t tiles_len, int32_t* chunk_base, void* stream) {
-  clear_error();
+    int64_t tiles_len, int32_t* chunk_base, bool noalloc, void* stream) {
   ASTRAI_REQUIRE(n_tokens >= 0 && n_tokens * (int64_t)top_k < (1ll << 31),
-                 "permute: n_tokens * top_k must be in [0, 2^31) (got %lld)",
+                 "%s: n_tokens * top_k must be in [0, 2^31) (got %lld)", who,
                  (long long)(n_tokens * (int64_t)top_k));
   ASTRAI_REQUIRE(n_experts >= 1 && n_experts <= ASTRAI_MOE_MAX_EXPERTS,
-                 "permute: n_experts must be in [1, %d] (got %d)",
+                 "%s: n_experts must be in [1, %d] (got %d)", who,
                  ASTRAI_MOE_MAX_EXPERTS, n_experts);
   ASTRAI_REQUIRE(top_k >= 1 && top_k <= n_experts && top_k <= ASTRAI_MOE_MAX_TOPK,
-                 "permute: top_k must be in [1, min(n_experts, %d)] (got %d)",
+                 "%s: top_k must be in [1, min(n_experts, %d)] (got %d)", who,
                  ASTRAI_MOE_MAX_TOPK, top_k);
-  ASTRAI_REQUIRE(dim >= 1, "permute: dim must be >= 1");
-  ASTRAI_REQUIRE(block_m >= 1, "permute: block_m must be >= 1");
+  ASTRAI_REQUIRE(dim >= 1, "%s: dim must be >= 1", who);
+  ASTRAI_REQUIRE(block_m >= 1, "%s: block_m must be >= 1", who);
   const int64_t need = astrai_moe_tile_list_len(n_tokens, n_experts, top_k, block_m);
   ASTRAI_REQUIRE(tiles_len >= need,
-                 "permute: tile list holds %lld int32, needs %lld",
+                 "%s: tile list holds %lld int32, needs %lld", who,
                  (long long)tiles_len, (long long)need);
   ASTRAI_REQUIRE(topk_idx && topk_w && chunk_hist && (x || !x_perm) &&
                      expert_offsets && sorted_token && sorted_w && token_pos &&
-                     tiles && chunk_base,
-                 "permute: null buffer");
+                     tiles && (chunk_base || noalloc),
+                 "%s: null buffer", who);
+  if (noalloc) {
+    // checked before any HIP call: a problem too large for the library's
+    // scratch is refused without touching the device
+    const int64_t need_scratch = permute_scratch_ints(n_tokens, n_experts);
+    ASTRAI_REQUIRE(need_scratch <= ASTRAI_MOE_NOALLOC_SCRATCH_INTS,
+                   "%s: %lld tokens over %d experts need %lld int32 of scratch, "
+                   "the library's scratch holds %d (use astrai_moe_permute with a "
+                   "caller-provided chunk_base)",
+                   who, (long long)n_tokens, n_experts, (long long)need_scratch,
+                   ASTRAI_MOE_NOALLOC_SCRATCH_INTS);
+    if (int rc = noalloc_scratch(&chunk_base)) return rc;
+  }
   const int64_t capacity =
       (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -427,7 +490,33 @@ extern "C" int astrai_moe_permute(
                                  n_experts, top_k, dim, block_m, expert_offsets,
                                  sorted_token, sorted_w, token_pos, x_perm, tiles,
                                  capacity, chunk_base, s);
-  return fail(ASTRAI_MOE_EINVAL, "permute: unsupported dtype %d", dtype);
+  return fail(ASTRAI_MOE_EINVAL, "%s: unsupported dtype %d", who, dtype);
+}
+
+extern "C" int astrai_moe_permute(
+    const int32_t* topk_idx, const void* topk_w, const int32_t* chunk_hist,
+    const void* x, int dtype, int64_t n_tokens, int n_experts, int top_k,
+    int64_t dim, int block_m, int32_t* expert_offsets, int32_t* sorted_token,
+    void* sorted_w, int32_t* token_pos, void* x_perm, int32_t* tiles,
+    int64_t tiles_len, int32_t* chunk_base, void* stream) {
+  clear_error();
+  return permute_impl("permute", topk_idx, topk_w, chunk_hist, x, dtype,
+                      n_tokens, n_experts, top_k, dim, block_m, expert_offsets,
+                      sorted_token, sorted_w, token_pos, x_perm, tiles,
+                      tiles_len, chunk_base, false, stream);
+}
+
+extern "C" int astrai_moe_permute_noalloc(
+    const int32_t* topk_idx, const void* topk_w, const int32_t* chunk_hist,
+    const void* x, int dtype, int64_t n_tokens, int n_experts, int top_k,
+    int64_t dim, int block_m, int32_t* expert_offsets, int32_t* sorted_token,
+    void* sorted_w, int32_t* token_pos, void* x_perm, int32_t* tiles,
+    int64_t tiles_len, void* stream) {
+  clear_error();
+  return permute_impl("permute_noalloc", topk_idx, topk_w, chunk_hist, x,
+                      dtype, n_tokens, n_experts, top_k, dim, block_m,
+                      expert_offsets, sorted_token, sorted_w, token_pos,
+                      x_perm, tiles, tiles_len, nullptr, true, stream);
 }
 
 extern "C" int astrai_moe_dense_tiles(int64_t n_rows, int block_m,

@@ -50,6 +50,10 @@ _SIGNATURES: dict[str, tuple] = {
         _int,
         [_vp, _vp, _vp, _vp, _int, _i64, _int, _int, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp],
     ),
+    "astrai_moe_permute_noalloc": (
+        _int,
+        [_vp, _vp, _vp, _vp, _int, _i64, _int, _int, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp],
+    ),
     "astrai_moe_gemm_gate_up": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp]),
     "astrai_moe_gemm_down": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp]),
     "astrai_moe_combine": (_int, [_vp, _vp, _vp, _int, _int, _i64, _int, _i64, _vp, _vp]),

@@ -124,6 +124,36 @@ int astrai_moe_permute(const int32_t* topk_idx, const void* topk_w,
                        int64_t tiles_len, int32_t* chunk_base, void* stream);
 
 /*
+ * astrai_moe_permute without the chunk_base workspace, for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference: its
+ * permutation (mlp.py:90-95) allocates through torch on every call.
+ * Same arguments, results (bit-identical) and errors as astrai_moe_permute,
+ * minus chunk_base: the scan's scratch is a fixed array inside the library,
+ * ASTRAI_MOE_NOALLOC_SCRATCH_INTS int32 per GPU, held from the first call on
+ * a GPU until the process ends. The call allocates nothing; the caller still
+ * provides every output.
+ *
+ * Limit: n_experts * ceil(n_chunks / r) int32 must fit the scratch, with
+ * n_chunks = ceil(n_tokens / ASTRAI_MOE_CHUNK_TOKENS) and r = 1, or r = 8 when
+ * n_chunks exceeds 32 * (1024 / next_pow2(n_experts)): e.g. 262144 tokens over
+ * 1024 experts, or 4 M tokens over 64. Larger problems return
+ * ASTRAI_MOE_EINVAL before any device work.
+ * Calls on one GPU share the scratch: calls that overlap (two streams, two
+ * host threads) race and must be serialised by the caller. Nothing in the
+ * scratch needs clearing between calls.
+ */
+#define ASTRAI_MOE_NOALLOC_SCRATCH_INTS (1 << 20)
+int astrai_moe_permute_noalloc(const int32_t* topk_idx, const void* topk_w,
+                               const int32_t* chunk_hist, const void* x,
+                               int dtype, int64_t n_tokens, int n_experts,
+                               int top_k, int64_t dim, int block_m,
+                               int32_t* expert_offsets, int32_t* sorted_token,
+                               void* sorted_w, int32_t* token_pos,
+                               void* x_perm, int32_t* tiles, int64_t tiles_len,
+                               void* stream);
+
+/*
  * Tile list of one dense expert over n_rows rows: every row belongs to expert
  * 0, in ceil(n_rows / block_m) row tiles (layout above), and, when
  * expert_offsets is not NULL, its offsets {0, n_rows} (int32[2]). With
