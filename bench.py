@@ -10,8 +10,9 @@ Prints one JSON line:
                   kernel time), and its fraction of the 2.5 PFLOP/s dense-bf16
                   matrix-core peak
   roofline        the dominant kernel (grouped gate/up GEMM): algorithmic
-                  FLOPs per launch / its average launch time, measured with
-                  HIP events on the launch stream over the instrumented pass
+                  FLOPs (or bytes) per launch / its average launch time,
+                  measured with HIP events on the launch stream around each
+                  launch in an instrumented pass of the layer forward
   kernels_ms      average time of every stage
   cpu_baseline    the reference path (the oracle's torch restatement of
                   mlp.py:64-100) on the host CPU, on a bounded token sample of
@@ -38,12 +39,17 @@ PEAK_HBM_GBS = 8000.0
 
 # Bytes moved between L2 and memory per launch of the dominant kernel (the
 # grouped gate/up GEMM), measured with rocprofv3 --pmc: FETCH_SIZE x 2 +
-# WRITE_SIZE (KiB). A 1 GiB device copy in the same run reads back as
-# FETCH_SIZE = 0.5 GiB and WRITE_SIZE = 1 GiB, so FETCH_SIZE is scaled by 2
-# (it counts this part's 128-byte read requests as 64 bytes). Source:
-# profiles/moe_layer_d4096_f14336_e8_k2_t16384.md.
+# WRITE_SIZE (KiB, median per dispatch). A device copy in the same run reads
+# back as FETCH_SIZE = half and WRITE_SIZE = all of its bytes (FETCH_SIZE
+# counts this part's 128-byte read requests as 64 bytes), hence the 2. Sources:
+# profiles/moe_layer_*.md of each workload.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
-    "moe_bf16_d4096_f14336_e8_k2_t16384": (6155562.2 * 2 + 917507.1) * 1024,
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (6155726.1 * 2 + 917505.3) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192": (779643.7 * 2 + 135168.2) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (760612.6 * 2 + 135168.1) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t64": (1567091.9 * 2 + 1539.5) * 1024,
+    # midpoint of the two counter runs in that profile (1,944,352-1,974,321 KiB)
+    "moe_bf16_d4096_f1536_e128_k8_t1024": (1959336.5 * 2 + 24609.0) * 1024,
 }
 
 
@@ -298,25 +304,29 @@ def main():
     flops_down = 2.0 * rows * w.dim * w.dim_ffn
     t_gu, t_dn = stage_ms["moe_gemm_gate_up"] / 1e3, stage_ms["moe_gemm_down"] / 1e3
     gemm_tflops = (flops_gate_up + flops_down) / (t_gu + t_dn) / 1e12
-    achieved = flops_gate_up / t_gu / 1e12
+    t_roof = t_gu  # the dominant kernel's average launch duration
     n_active = int((counts > 0).sum().item())
     weight_bytes = n_active * 3.0 * w.dim * w.dim_ffn * s
     bytes_permute = T * w.dim * s + rows * w.dim * s + rows * 8
     bytes_combine = rows * w.dim * s + T * w.dim * s + rows * (s + 8)
     traffic = MEASURED_TRAFFIC_BYTES.get(name)
     block_m = ops.select_block_m(T, w.n_experts, w.top_k, w.dim, w.dim_ffn, w.dtype)
+    timing = f"HIP events on the launch stream around each of its {args.steps} launches in the layer forward"
     if bf16 and block_m in (32, 64):
         # decode- and mid-sized loads: the gate/up kernel streams the routed experts' weights
         gu_bytes = n_active * 2.0 * w.dim * w.dim_ffn * s + rows * w.dim * s + rows * w.dim_ffn * s
-        gbs = gu_bytes / t_gu / 1e9
-        roofline = {"kernel": "gemm_mfma_kernel<gate_up" + (", gather>" if gathered else ">"), "bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS, "traffic": traffic,
-                    "algorithmic_bytes_per_launch": gu_bytes}
+        gbs = gu_bytes / t_roof / 1e9
+        roofline = {"kernel": "gemm_mfma_kernel<gate_up" + (", gather>" if gathered else ">"), "bound": "hbm",
+                    "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+                    "traffic": traffic, "algorithmic_bytes_per_launch": gu_bytes, "kernel_ms": t_gu * 1e3,
+                    "timing": timing}
     else:
+        achieved = flops_gate_up / t_roof / 1e12
         roofline = {"kernel": (("gemm_stream_kernel<gate_up, gather>" if gathered else "gemm_stream_kernel<gate_up>")
                                if bf16 else "gemm_generic_kernel<gate_up>"),
                     "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
-                    "traffic": traffic, "algorithmic_flops_per_launch": flops_gate_up}
+                    "traffic": traffic, "algorithmic_flops_per_launch": flops_gate_up, "kernel_ms": t_gu * 1e3,
+                    "timing": timing}
 
     result = {
         "metric": "MoE-layer tokens/s + grouped-GEMM TFLOP/s (% of bf16 MFMA peak), 1 GPU",
