@@ -69,6 +69,17 @@ __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) {
   return (a + b - 1) / b;
 }
 
+// Position of the gate (or up) projection of column c in a training
+// forward's saved gu row of 2 n values: columns go in blocks of 4, each block
+// as its gate values followed by the same columns' up values; the last block
+// holds the n % 4 columns left (when n is not a multiple of 4). For n a
+// multiple of 4: g[c .. c+3] at 2 c, u[c .. c+3] at 2 c + 4.
+__host__ __device__ inline int64_t gu_index(int64_t c, int64_t n, bool up) {
+  const int64_t b = c >> 2;
+  const int64_t w = n - 4 * b < 4 ? n - 4 * b : 4;
+  return 8 * b + (up ? w : 0) + (c & 3);
+}
+
 // ---------------------------------------------------------------------------
 // Host side: per-thread error message and launch checking (capi.hip).
 // ---------------------------------------------------------------------------

@@ -78,6 +78,25 @@ int launch_wgrad(const void* a, const void* b, const int32_t* offsets,
                  int n_experts, int64_t m, int64_t n, void* dw,
                  hipStream_t s);
 
+// General-shape backward (moe_gemm_generic_bwd.hip): fp32 or bf16, any dim
+// and dim_ffn, any row-tile height; same contracts as the matrix-core ones
+// above, the saved gu in the blocked layout of gu_index.
+int launch_generic_dgrad_down(int dtype, const void* dy, const int32_t* tiles,
+                              int64_t capacity, const void* const* w_down,
+                              const void* gu, int64_t dim, int64_t dim_ffn,
+                              void* dg, void* du, hipStream_t s);
+int launch_generic_dgrad_in(int dtype, const void* d, const int32_t* tiles,
+                            int64_t capacity, const void* const* w, int64_t k,
+                            int64_t n, const void* add, void* dx,
+                            hipStream_t s);
+int launch_generic_wgrad(int dtype, const void* a, const void* b,
+                         const int32_t* offsets, int n_experts, int64_t m,
+                         int64_t n, void* dw, hipStream_t s);
+int launch_generic_row_grad(int dtype, const void* dout,
+                            const int32_t* sorted_token, const void* sorted_w,
+                            const void* y, int64_t n_rows, int64_t dim,
+                            void* dy, void* dw_rows, hipStream_t s);
+
 // Packs one expert's weight for the packed GEMMs: gate/up (w0 = gate, w1 =
 // up, each [rows, k]) or down (w0 = [rows, k]).
 int launch_pack(const void* w0, const void* w1, int64_t rows, int64_t k,

@@ -32,11 +32,16 @@ constexpr int kGenBM = 64;
 constexpr int kGenBN = 64;
 constexpr int kGenBK = 16;
 
-template <typename T, bool kGateUp>
+// kSave (training forward): also store what the backward needs — for gate/up
+// the rounded gate and up projections in S0 [rows, 2 N] in the blocked
+// layout of gu_index, for down the rounded output before the routing weight
+// in S0 [rows, N].
+template <typename T, bool kGateUp, bool kSave = false>
 __global__ __launch_bounds__(kGenThreads) void gemm_generic_kernel(
     const T* __restrict__ A, const int32_t* __restrict__ tiles,
     const void* const* __restrict__ W0, const void* const* __restrict__ W1,
-    const T* __restrict__ row_w, int64_t K, int64_t N, T* __restrict__ C) {
+    const T* __restrict__ row_w, int64_t K, int64_t N, T* __restrict__ C,
+    T* __restrict__ S0 = nullptr) {
   const int tile = blockIdx.x;
   const int n_live = min(tiles[0], tiles[2]);
   if (tile >= n_live) return;
@@ -112,7 +117,13 @@ __global__ __launch_bounds__(kGenThreads) void gemm_generic_kernel(
           const float u = Elem<T>::round(acc1[i][j]);
           const float s = Elem<T>::round(silu_f32(g));
           v = u * s;
+          if constexpr (kSave) {
+            T* gu = S0 + (row0 + r) * 2 * N;
+            gu[gu_index(n, N, false)] = Elem<T>::from_f32(g);
+            gu[gu_index(n, N, true)] = Elem<T>::from_f32(u);
+          }
         } else {
+          if constexpr (kSave) S0[(row0 + r) * N + n] = Elem<T>::from_f32(acc0[i][j]);
           // no row weights (a dense expert): weight 1, an exact product
           v = Elem<T>::round(acc0[i][j]) * (row_w ? Elem<T>::to_f32(row_w[row0 + r]) : 1.0f);
         }
@@ -122,16 +133,17 @@ __global__ __launch_bounds__(kGenThreads) void gemm_generic_kernel(
   }
 }
 
-template <typename T, bool kGateUp>
+template <typename T, bool kGateUp, bool kSave = false>
 int launch_generic(const void* A, const int32_t* tiles, int64_t capacity,
                    const void* const* W0, const void* const* W1,
                    const void* row_w, int64_t K, int64_t N, void* C,
-                   hipStream_t s) {
+                   hipStream_t s, void* S0 = nullptr) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   const dim3 grid((unsigned)capacity, (unsigned)ceil_div(N, kGenBN));
-  hipLaunchKernelGGL((gemm_generic_kernel<T, kGateUp>), grid, dim3(kGenThreads), 0,
+  hipLaunchKernelGGL((gemm_generic_kernel<T, kGateUp, kSave>), grid, dim3(kGenThreads), 0,
                      s, static_cast<const T*>(A), tiles, W0, W1,
-                     static_cast<const T*>(row_w), K, N, static_cast<T*>(C));
+                     static_cast<const T*>(row_w), K, N, static_cast<T*>(C),
+                     static_cast<T*>(S0));
   return check_launch(kGateUp ? "gemm_generic_kernel<gate_up>"
                               : "gemm_generic_kernel<down>");
 }
@@ -301,16 +313,22 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
 }
 
 // ---------------------------------------------------------------------------
-// Training forward and backward (bf16, matrix-core shapes, 256-row tiles).
+// Training forward and backward. bf16 with dim % 256 == 0 and dim_ffn % 128 ==
+// 0 runs the matrix-core kernels (256-row tile lists); every other shape and
+// fp32 runs the general-shape kernels (any tile height).
 // ---------------------------------------------------------------------------
 
+static bool mfma_train_shape(int dtype, int64_t dim, int64_t dim_ffn) {
+  return dtype == ASTRAI_MOE_BF16 && dim > 0 && dim_ffn > 0 && dim % 256 == 0 && dim_ffn % 128 == 0 &&
+         dim <= (1ll << 22) && dim_ffn <= (1ll << 22);
+}
+
 static int check_train(const char* who, int dtype, int64_t dim, int64_t dim_ffn, int block_m) {
-  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "%s: the backward kernels are bf16 only (dtype %d)", who, dtype);
-  ASTRAI_REQUIRE(block_m == kMfmaBigBM, "%s: needs the 256-row tile list (block_m %d)", who, block_m);
-  ASTRAI_REQUIRE(dim > 0 && dim_ffn > 0 && dim % 256 == 0 && dim_ffn % 128 == 0 && dim <= (1ll << 22) &&
-                     dim_ffn <= (1ll << 22),
-                 "%s: needs dim %% 256 == 0 and dim_ffn %% 128 == 0 (got %lld, %lld)", who, (long long)dim,
-                 (long long)dim_ffn);
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16 || dtype == ASTRAI_MOE_F32, "%s: unsupported dtype %d", who, dtype);
+  ASTRAI_REQUIRE(dim > 0 && dim_ffn > 0, "%s: dims must be >= 1", who);
+  if (mfma_train_shape(dtype, dim, dim_ffn))
+    ASTRAI_REQUIRE(block_m == kMfmaBigBM, "%s: bf16 matrix-core shapes need the 256-row tile list (block_m %d)", who,
+                   block_m);
   return ASTRAI_MOE_OK;
 }
 
@@ -325,11 +343,17 @@ extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* 
   if ((rc = check_train("gemm_gate_up_train", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_gate && w_up && gu, "gemm_gate_up_train: null weight table or output");
-  ASTRAI_REQUIRE(aligned16_ptr(x_perm) && aligned16_ptr(h) && aligned16_ptr(gu),
-                 "gemm_gate_up_train: buffers must be 16-byte aligned");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
-  return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, gu,
-                                  static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma_train_shape(dtype, dim, dim_ffn)) {
+    ASTRAI_REQUIRE(aligned16_ptr(x_perm) && aligned16_ptr(h) && aligned16_ptr(gu),
+                   "gemm_gate_up_train: buffers must be 16-byte aligned");
+    return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, gu, s);
+  }
+  if (dtype == ASTRAI_MOE_BF16)
+    return launch_generic<bf16_t, true, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
+                                              gu);
+  return launch_generic<float, true, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, gu);
 }
 
 extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, int64_t tiles_len,
@@ -342,26 +366,34 @@ extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, i
   if ((rc = check_train("gemm_down_train", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_down && sorted_w && y_unweighted, "gemm_down_train: null weight table, row weights or output");
-  ASTRAI_REQUIRE(aligned16_ptr(h) && aligned16_ptr(y) && aligned16_ptr(y_unweighted),
-                 "gemm_down_train: buffers must be 16-byte aligned");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
-  return launch_mfma_down_save(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, y, y_unweighted,
-                               static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma_train_shape(dtype, dim, dim_ffn)) {
+    ASTRAI_REQUIRE(aligned16_ptr(h) && aligned16_ptr(y) && aligned16_ptr(y_unweighted),
+                   "gemm_down_train: buffers must be 16-byte aligned");
+    return launch_mfma_down_save(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, y, y_unweighted, s);
+  }
+  if (dtype == ASTRAI_MOE_BF16)
+    return launch_generic<bf16_t, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
+                                               y_unweighted);
+  return launch_generic<float, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
+                                            y_unweighted);
 }
 
 extern "C" int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token, const void* sorted_w,
                                    const void* y_unweighted, int dtype, int64_t n_rows, int64_t dim, void* dy,
                                    void* dw_rows, void* stream) {
   clear_error();
-  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "row_grad: bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16 || dtype == ASTRAI_MOE_F32, "row_grad: unsupported dtype %d", dtype);
   ASTRAI_REQUIRE(n_rows >= 0 && n_rows < (1ll << 31), "row_grad: n_rows must be in [0, 2^31)");
-  ASTRAI_REQUIRE(dim > 0 && dim % 8 == 0, "row_grad: needs dim %% 8 == 0 (got %lld)", (long long)dim);
+  ASTRAI_REQUIRE(dim > 0, "row_grad: dim must be >= 1 (got %lld)", (long long)dim);
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(dout && sorted_token && sorted_w && y_unweighted && dy && dw_rows, "row_grad: null buffer");
-  ASTRAI_REQUIRE(aligned16_ptr(dout) && aligned16_ptr(y_unweighted) && aligned16_ptr(dy),
-                 "row_grad: buffers must be 16-byte aligned");
-  return launch_row_grad(dout, sorted_token, sorted_w, y_unweighted, n_rows, dim, dy, dw_rows,
-                         static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ASTRAI_MOE_BF16 && dim % 8 == 0 && aligned16_ptr(dout) && aligned16_ptr(y_unweighted) &&
+      aligned16_ptr(dy))
+    return launch_row_grad(dout, sorted_token, sorted_w, y_unweighted, n_rows, dim, dy, dw_rows, s);
+  return launch_generic_row_grad(dtype, dout, sorted_token, sorted_w, y_unweighted, n_rows, dim, dy, dw_rows, s);
 }
 
 extern "C" int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles, int64_t tiles_len,
@@ -375,10 +407,14 @@ extern "C" int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles, 
   if ((rc = check_train("gemm_dgrad_down", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_down && gu && du, "gemm_dgrad_down: null weight table or buffer");
-  ASTRAI_REQUIRE(aligned16_ptr(dy) && aligned16_ptr(gu) && aligned16_ptr(dg) && aligned16_ptr(du),
-                 "gemm_dgrad_down: buffers must be 16-byte aligned");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
-  return launch_dgrad_down(dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma_train_shape(dtype, dim, dim_ffn)) {
+    ASTRAI_REQUIRE(aligned16_ptr(dy) && aligned16_ptr(gu) && aligned16_ptr(dg) && aligned16_ptr(du),
+                   "gemm_dgrad_down: buffers must be 16-byte aligned");
+    return launch_dgrad_down(dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, s);
+  }
+  return launch_generic_dgrad_down(dtype, dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, s);
 }
 
 extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, const int32_t* tiles, int64_t tiles_len,
@@ -392,27 +428,33 @@ extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, con
   if ((rc = check_train("gemm_dgrad_gate_up", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(du && w_gate && w_up, "gemm_dgrad_gate_up: null weight table or buffer");
-  ASTRAI_REQUIRE(aligned16_ptr(dg) && aligned16_ptr(du) && aligned16_ptr(dx_perm),
-                 "gemm_dgrad_gate_up: buffers must be 16-byte aligned");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // dx_perm = bf16(dg . W_gate), then dx_perm = bf16(bf16(du . W_up) + dx_perm)
-  if ((rc = launch_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
-  return launch_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
+  // dx_perm = round(dg . W_gate), then dx_perm = round(round(du . W_up) + dx_perm)
+  if (mfma_train_shape(dtype, dim, dim_ffn)) {
+    ASTRAI_REQUIRE(aligned16_ptr(dg) && aligned16_ptr(du) && aligned16_ptr(dx_perm),
+                   "gemm_dgrad_gate_up: buffers must be 16-byte aligned");
+    if ((rc = launch_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
+    return launch_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
+  }
+  if ((rc = launch_generic_dgrad_in(dtype, dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
+  return launch_generic_dgrad_in(dtype, du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
 }
 
 extern "C" int astrai_moe_gemm_wgrad(const void* a, const void* b, const int32_t* expert_offsets, int dtype,
                                      int64_t n_rows, int n_experts, int64_t m, int64_t n, void* dw, void* stream) {
   clear_error();
-  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_wgrad: bf16 only (dtype %d)", dtype);
+  ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16 || dtype == ASTRAI_MOE_F32, "gemm_wgrad: unsupported dtype %d", dtype);
   ASTRAI_REQUIRE(n_rows >= 0 && n_rows < (1ll << 31), "gemm_wgrad: n_rows must be in [0, 2^31)");
   ASTRAI_REQUIRE(n_experts >= 1 && n_experts <= ASTRAI_MOE_MAX_EXPERTS, "gemm_wgrad: n_experts must be in [1, %d]",
                  ASTRAI_MOE_MAX_EXPERTS);
-  ASTRAI_REQUIRE(m > 0 && n > 0 && m % 8 == 0 && n % 8 == 0 && m <= (1ll << 22) && n <= (1ll << 22),
-                 "gemm_wgrad: needs m %% 8 == 0 and n %% 8 == 0 (got %lld, %lld)", (long long)m, (long long)n);
+  ASTRAI_REQUIRE(m > 0 && n > 0 && m <= (1ll << 22) && n <= (1ll << 22),
+                 "gemm_wgrad: m and n must be in [1, 2^22] (got %lld, %lld)", (long long)m, (long long)n);
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(a && b && expert_offsets && dw, "gemm_wgrad: null buffer");
-  ASTRAI_REQUIRE(aligned16_ptr(a) && aligned16_ptr(b) && aligned16_ptr(dw),
-                 "gemm_wgrad: buffers must be 16-byte aligned");
-  return launch_wgrad(a, b, expert_offsets, n_experts, m, n, dw, static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == ASTRAI_MOE_BF16 && m % 8 == 0 && n % 8 == 0 && aligned16_ptr(a) && aligned16_ptr(b) &&
+      aligned16_ptr(dw))
+    return launch_wgrad(a, b, expert_offsets, n_experts, m, n, dw, s);
+  return launch_generic_wgrad(dtype, a, b, expert_offsets, n_experts, m, n, dw, s);
 }

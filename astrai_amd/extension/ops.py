@@ -436,13 +436,19 @@ def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tens
 # -- training: forward that keeps g, u, y and the backward kernels ------------
 
 
-def backward_supported(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
-    """Whether the grouped backward kernels take this expert shape (bf16 and
-    the matrix-core shapes; they run on 256-row tile lists)."""
+def backward_on_matrix_cores(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
+    """Whether training runs the matrix-core kernels for this expert shape
+    (bf16, dim % 256 == 0, dim_ffn % 128 == 0; 256-row tile lists). Every
+    other shape and fp32 runs the general-shape kernels."""
     return packed_supported(dim, dim_ffn, dtype)
 
 
-TRAIN_BLOCK_M = 256
+TRAIN_BLOCK_M = 256  # row-tile height of the matrix-core training kernels
+
+
+def train_block_m(dim: int, dim_ffn: int, dtype: torch.dtype) -> int:
+    """Row-tile height of the training forward and backward for this shape."""
+    return TRAIN_BLOCK_M if backward_on_matrix_cores(dim, dim_ffn, dtype) else 64
 
 
 def _lib_call(name: str, *args) -> None:
@@ -451,28 +457,38 @@ def _lib_call(name: str, *args) -> None:
 
 def moe_gemm_gate_up_train(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
                            n_experts: int, dim_ffn: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """``h`` as ``moe_gemm_gate_up`` plus ``gu [rows, 2 * dim_ffn]``, the bf16
-    gate and up projections the backward needs, interleaved per 4 columns
-    (``gu_split`` separates them); 256-row tile list."""
+    """``h`` as ``moe_gemm_gate_up`` plus ``gu [rows, 2 * dim_ffn]``, the
+    rounded gate and up projections the backward needs, in blocks of 4 columns
+    (``gu_split`` separates them); tile list at ``train_block_m``'s height."""
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
     n_rows, dim = x_perm.shape
-    _check_tiles(tiles, TRAIN_BLOCK_M, x_perm, "moe_gemm_gate_up_train")
+    bm = train_block_m(dim, dim_ffn, x_perm.dtype)
+    _check_tiles(tiles, bm, x_perm, "moe_gemm_gate_up_train")
     _require_table(w_gate, "w_gate", n_experts, x_perm)
     _require_table(w_up, "w_up", n_experts, x_perm)
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     gu = torch.empty(n_rows, 2 * dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     _lib_call("astrai_moe_gemm_gate_up_train", x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
-              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, h.data_ptr(), gu.data_ptr(),
+              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, bm, h.data_ptr(), gu.data_ptr(),
               _stream(x_perm))
     return h, gu
 
 
 def gu_split(gu: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """``(g, u)`` views of the interleaved projections of ``moe_gemm_gate_up_train``."""
+    """``(g, u)`` of the saved projections of ``moe_gemm_gate_up_train``:
+    columns in blocks of 4, each block's gate values then the same columns' up
+    values, the last block holding the ``dim_ffn % 4`` columns left."""
     rows, two_f = gu.shape
-    v = gu.view(rows, two_f // 8, 2, 4)
-    return v[:, :, 0, :].reshape(rows, two_f // 2), v[:, :, 1, :].reshape(rows, two_f // 2)
+    f = two_f // 2
+    q = f // 4
+    head = gu[:, :8 * q].reshape(rows, q, 2, 4)
+    g, u = head[:, :, 0, :].reshape(rows, 4 * q), head[:, :, 1, :].reshape(rows, 4 * q)
+    w = f - 4 * q
+    if w:
+        tail = gu[:, 8 * q:]
+        g, u = torch.cat([g, tail[:, :w]], 1), torch.cat([u, tail[:, w:]], 1)
+    return g, u
 
 
 def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor,
@@ -483,11 +499,12 @@ def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tens
     n_rows, dim_ffn = h.shape
     if sorted_w.numel() != n_rows or sorted_w.dtype != h.dtype:
         raise ValueError("sorted_w must hold one weight of h's dtype per row")
-    _check_tiles(tiles, TRAIN_BLOCK_M, h, "moe_gemm_down_train")
+    bm = train_block_m(dim, dim_ffn, h.dtype)
+    _check_tiles(tiles, bm, h, "moe_gemm_down_train")
     _require_table(w_down, "w_down", n_experts, h)
     y, y_unw = (torch.empty(n_rows, dim, dtype=h.dtype, device=h.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_down_train", h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
-              sorted_w.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, TRAIN_BLOCK_M, y.data_ptr(),
+              sorted_w.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, bm, y.data_ptr(),
               y_unw.data_ptr(), _stream(h))
     return y, y_unw
 
@@ -516,11 +533,12 @@ def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Ten
     code = _dtype_code(dy, "dy")
     n_rows, dim = dy.shape
     dim_ffn = gu.shape[1] // 2
-    _check_tiles(tiles, TRAIN_BLOCK_M, dy, "moe_gemm_dgrad_down")
+    bm = train_block_m(dim, dim_ffn, dy.dtype)
+    _check_tiles(tiles, bm, dy, "moe_gemm_dgrad_down")
     _require_table(w_down, "w_down", n_experts, dy)
     dg, du = (torch.empty(n_rows, dim_ffn, dtype=dy.dtype, device=dy.device) for _ in range(2))
     _lib_call("astrai_moe_gemm_dgrad_down", dy.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
-              gu.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, TRAIN_BLOCK_M, dg.data_ptr(), du.data_ptr(),
+              gu.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, bm, dg.data_ptr(), du.data_ptr(),
               _stream(dy))
     return dg, du
 
@@ -531,12 +549,13 @@ def moe_gemm_dgrad_gate_up(dg: torch.Tensor, du: torch.Tensor, tiles: torch.Tens
     _require_gpu(dg, "dg", 2)
     code = _dtype_code(dg, "dg")
     n_rows, dim_ffn = dg.shape
-    _check_tiles(tiles, TRAIN_BLOCK_M, dg, "moe_gemm_dgrad_gate_up")
+    bm = train_block_m(dim, dim_ffn, dg.dtype)
+    _check_tiles(tiles, bm, dg, "moe_gemm_dgrad_gate_up")
     _require_table(w_gate, "w_gate", n_experts, dg)
     _require_table(w_up, "w_up", n_experts, dg)
     dx = torch.empty(n_rows, dim, dtype=dg.dtype, device=dg.device)
     _lib_call("astrai_moe_gemm_dgrad_gate_up", dg.data_ptr(), du.data_ptr(), tiles.data_ptr(), tiles.numel(),
-              w_gate.data_ptr(), w_up.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, TRAIN_BLOCK_M,
+              w_gate.data_ptr(), w_up.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, bm,
               dx.data_ptr(), _stream(dg))
     return dx
 

@@ -23,7 +23,8 @@ The HIP path is the only path: inputs it cannot take (CPU tensors, dtypes
 other than float32/bfloat16, experts whose ``up/gate/down`` are not bias-free
 ``Linear`` modules, e.g. after LoRA injection) raise instead of silently
 running something else. With autograd active the forward still runs on the
-kernels and the backward recomputes the experts (``autograd.py``).
+kernels and so does the backward (grouped dgrad / wgrad kernels,
+``autograd.py``).
 """
 
 from __future__ import annotations
@@ -243,7 +244,7 @@ class DeepSeekMoE(nn.Module):
                                       packed=packed)
 
     def _forward_autograd(self, x: Tensor) -> Tensor:
-        """mlp.py:64-100 with autograd: kernels forward, recompute backward.
+        """mlp.py:64-100 with autograd: HIP kernels forward and backward.
         Routing indices come from the route kernel; the weights are rebuilt
         from the logits with torch ops (same values) so their gradient reaches
         the router."""

@@ -292,8 +292,10 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
  * Training: forward that keeps what the backward needs, and the backward.
  * The reference gets its gradients from torch autograd over mlp.py:22-25
  * and :89-98; these entry points compute the same quantities with grouped
- * kernels (bf16 only; dim % 256 == 0, dim_ffn % 128 == 0; tile lists built
- * with block_m = 256). Per expert e with permuted rows R_e:
+ * kernels, at autograd's rounding points (identities in fp32): on the matrix
+ * cores for bf16 with dim % 256 == 0 and dim_ffn % 128 == 0 (tile lists built
+ * with block_m = 256), on the general-shape kernels for every other shape and
+ * for fp32 (any block_m). Per expert e with permuted rows R_e:
  *
  *   forward   g = x W_gate^T, u = x W_up^T, h = u * silu(g), y = h W_down^T,
  *             out = sum over slots of y * w                    (mlp.py:22-24, :97-98)
@@ -303,11 +305,13 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
  *             dW_down[e] = dy^T h,  dW_gate[e] = dg^T x_perm,  dW_up[e] = du^T x_perm
  *
  * astrai_moe_gemm_gate_up_train: astrai_moe_gemm_gate_up plus gu
- *   ([n_rows, 2 dim_ffn] bf16: the rounded projections silu and the product
- *   use, interleaved per 4 columns: gu[r, 2c .. 2c+3] = g[r, c .. c+3] and
- *   gu[r, 2c+4 .. 2c+7] = u[r, c .. c+3] for c a multiple of 4).
+ *   ([n_rows, 2 dim_ffn] dtype: the rounded projections silu and the product
+ *   use, in blocks of 4 columns: gu[r, 2c .. 2c+3] = g[r, c .. c+3] and
+ *   gu[r, 2c+4 .. 2c+7] = u[r, c .. c+3] for c a multiple of 4; when dim_ffn
+ *   is not a multiple of 4, the last block holds its w = dim_ffn % 4 columns
+ *   as g then u, w values each).
  * astrai_moe_gemm_down_train: astrai_moe_gemm_down plus y_unweighted
- *   ([n_rows, dim] bf16, the rounded expert output before the routing weight).
+ *   ([n_rows, dim] dtype, the rounded expert output before the routing weight).
  */
 int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles,
                                   int64_t tiles_len, const void* const* w_gate,
@@ -324,9 +328,10 @@ int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles,
 
 /*
  * Per permuted row r (token sorted_token[r], weight sorted_w[r]):
- *   dy[r]      = dout[token] * w, rounded per element     [n_rows, dim] bf16
- *   dw_rows[r] = sum_d bf16(dout[token, d] * y[r, d])     [n_rows] bf16
- * (mlp.py:97's expert_output * weights, differentiated in both factors).
+ *   dy[r]      = dout[token] * w, rounded per element     [n_rows, dim] dtype
+ *   dw_rows[r] = sum_d round(dout[token, d] * y[r, d])    [n_rows] dtype
+ * (mlp.py:97's expert_output * weights, differentiated in both factors;
+ * round() is the rounding to dtype, the identity in fp32).
  */
 int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token,
                         const void* sorted_w, const void* y_unweighted,
@@ -335,11 +340,11 @@ int astrai_moe_row_grad(const void* dout, const int32_t* sorted_token,
 
 /*
  * Grouped dgrad of the down projection with the SwiGLU backward fused:
- *   dh = dy . W_down[e] (W_down [dim, dim_ffn]), rounded to bf16, then
- *   du = bf16(dh * silu(g)), dg = bf16(bf16(dh * u) * silu'(g))
+ *   dh = dy . W_down[e] (W_down [dim, dim_ffn]), rounded to dtype, then
+ *   du = round(dh * silu(g)), dg = round(round(dh * u) * silu'(g))
  * (the order torch autograd takes through mlp.py:23).
  *   dy [n_rows, dim], gu [n_rows, 2 dim_ffn] (from astrai_moe_gemm_gate_up_train),
- *   dg, du [n_rows, dim_ffn], all bf16.
+ *   dg, du [n_rows, dim_ffn], all dtype.
  */
 int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles,
                                int64_t tiles_len, const void* const* w_down,
@@ -350,7 +355,7 @@ int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles,
 
 /*
  * Grouped dgrad of the gate and up projections:
- *   dx_perm = bf16(bf16(dg . W_gate[e]) + bf16(du . W_up[e]))   [n_rows, dim] bf16
+ *   dx_perm = round(round(dg . W_gate[e]) + round(du . W_up[e]))   [n_rows, dim] dtype
  * (autograd's rounding: each linear's input gradient, then their sum).
  */
 int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du,
@@ -364,8 +369,9 @@ int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du,
 /*
  * Per-expert weight gradient: dw[e] = a[rows of e]^T . b[rows of e], the rows
  * of expert e being expert_offsets[e] .. expert_offsets[e + 1] - 1.
- *   a [n_rows, m], b [n_rows, n], dw [n_experts, m, n], all bf16 (m % 8 == 0,
- *   n % 8 == 0). Experts without rows are not written.
+ *   a [n_rows, m], b [n_rows, n], dw [n_experts, m, n], all dtype (the
+ *   matrix-core kernel for bf16 with m % 8 == 0 and n % 8 == 0, the
+ *   general-shape one otherwise). Experts without rows are not written.
  * dW_down: (a, b) = (dy, h); dW_gate: (dg, x_perm); dW_up: (du, x_perm).
  */
 int astrai_moe_gemm_wgrad(const void* a, const void* b,

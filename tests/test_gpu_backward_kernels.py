@@ -3,10 +3,14 @@ and of the training forward's saved tensors with torch on the same device.
 
 Each kernel is checked on its own inputs against a float32 torch evaluation of
 the formula torch autograd applies to mlp.py:22-25 and :97-98, at the
-reference's bf16 rounding points where the kernel reproduces them exactly
-(bit-exact checks) and otherwise within the layer's bf16 tolerance: elementwise
-|got - ref| <= 2e-2 |ref| + 1e-3 max|ref|, >= 99.9 % of the elements passing
-and the worst error below 5 % of max|ref|.
+reference's rounding points where the kernel reproduces them exactly
+(bit-exact checks) and otherwise within the layer's tolerance: elementwise
+|got - ref| <= rtol |ref| + atol max|ref| with (rtol, atol) = (2e-2, 1e-3) in
+bf16 and (1e-4, 1e-6) in fp32, >= 99.9 % of the elements passing and the worst
+error below 5 % (bf16) / 1e-4 (fp32) of max|ref|. The cases cover both kernel
+families: the matrix-core kernels (bf16, dim % 256 == 0, dim_ffn % 128 == 0)
+and the general-shape ones (fp32, other shapes, dim_ffn not a multiple of 4 —
+the saved projections' last block of columns then holds fewer than 4).
 """
 
 from __future__ import annotations
@@ -23,25 +27,27 @@ BF = torch.bfloat16
 
 
 def _close(got, ref, label):
+    fp32 = got.dtype == torch.float32
+    rtol, atol, worst_frac = (1e-4, 1e-6, 1e-4) if fp32 else (2e-2, 1e-3, 5e-2)
     got, ref = got.float(), ref.float()
     scale = ref.abs().max().item() or 1.0
     err = (got - ref).abs()
-    frac = (err <= 2e-2 * ref.abs() + 1e-3 * scale).float().mean().item()
+    frac = (err <= rtol * ref.abs() + atol * scale).float().mean().item()
     worst = err.max().item()
     assert frac >= 0.999, f"{label}: {frac:.5f} within tolerance (max err {worst:.3e}, scale {scale:.3e})"
-    assert worst <= 5e-2 * scale, f"{label}: max err {worst:.3e} vs scale {scale:.3e}"
+    assert worst <= worst_frac * scale, f"{label}: max err {worst:.3e} vs scale {scale:.3e}"
 
 
-def _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew=0.0, seed=0):
+def _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew=0.0, seed=0, dtype=BF):
     g = torch.Generator(device=gpu).manual_seed(seed)
     logits = torch.randn(n_tok, n_exp, generator=g, device=gpu)
     logits += skew * torch.log1p(torch.arange(n_exp, device=gpu, dtype=torch.float32)).neg()
-    route = ops.moe_route(logits.to(BF), top_k)
-    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(BF)
-    perm = ops.moe_permute(route, x, n_exp, ops.TRAIN_BLOCK_M)
+    route = ops.moe_route(logits.to(dtype), top_k)
+    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
+    perm = ops.moe_permute(route, x, n_exp, ops.train_block_m(dim, dim_ffn, dtype))
 
     def w(*shape):
-        return (torch.randn(*shape, generator=g, device=gpu) * 0.02).to(BF)
+        return (torch.randn(*shape, generator=g, device=gpu) * 0.02).to(dtype)
 
     wg = [w(dim_ffn, dim) for _ in range(n_exp)]
     wu = [w(dim_ffn, dim) for _ in range(n_exp)]
@@ -52,30 +58,37 @@ def _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew=0.0, seed=0):
 
 
 CASES = [
-    # (tokens, experts, top_k, dim, dim_ffn, skew)
-    (2048, 8, 2, 1024, 1536, 0.0),
-    (300, 16, 4, 512, 384, 0.0),  # partial 256-column tiles, ~75 rows per expert
-    (64, 128, 8, 256, 128, 0.0),  # a few rows per expert, some experts empty
-    (3000, 8, 2, 256, 640, 3.0),  # skewed: one expert holds most rows
+    # (tokens, experts, top_k, dim, dim_ffn, skew, dtype): matrix-core kernels
+    (2048, 8, 2, 1024, 1536, 0.0, BF),
+    (300, 16, 4, 512, 384, 0.0, BF),  # partial 256-column tiles, ~75 rows per expert
+    (64, 128, 8, 256, 128, 0.0, BF),  # a few rows per expert, some experts empty
+    (3000, 8, 2, 256, 640, 3.0, BF),  # skewed: one expert holds most rows
+    # general-shape kernels
+    (300, 8, 2, 40, 24, 0.0, BF),  # the reference's tiny-config scale
+    (200, 4, 2, 37, 30, 0.0, BF),  # dim_ffn % 4 == 2: a 2-column last block of g/u
+    (150, 6, 3, 13, 7, 0.0, torch.float32),  # dim_ffn % 4 == 3
+    (257, 8, 2, 64, 129, 0.0, torch.float32),  # dim_ffn % 4 == 1
+    (500, 8, 2, 256, 128, 2.0, torch.float32),  # a matrix-core shape in fp32, skewed
 ]
 
 
-@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn,skew", CASES)
-def test_backward_kernels(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew):
-    perm, (wg, wu, wd), (tg, tu, td), gen = _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew)
+@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn,skew,dtype", CASES)
+def test_backward_kernels(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew, dtype):
+    perm, (wg, wu, wd), (tg, tu, td), gen = _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew, dtype=dtype)
     E = n_exp
+    bm = ops.train_block_m(dim, dim_ffn, dtype)
     # training forward: h and y*w bit-identical to the inference kernels
     h, gu = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn)
     g, u = ops.gu_split(gu)
     y, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, E, dim)
-    h_inf = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn, ops.TRAIN_BLOCK_M)
-    y_inf = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, E, dim, ops.TRAIN_BLOCK_M)
+    h_inf = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn, bm)
+    y_inf = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, E, dim, bm)
     torch.cuda.synchronize()
     assert torch.equal(h, h_inf) and torch.equal(y, y_inf)
-    assert torch.equal(y, (y_unw.float() * perm.sorted_w.float().unsqueeze(-1)).to(BF))
+    assert torch.equal(y, (y_unw.float() * perm.sorted_w.float().unsqueeze(-1)).to(dtype))
 
     n_tokens = n_tok
-    dout = torch.randn(n_tokens, dim, generator=gen, device=gpu).to(BF)
+    dout = torch.randn(n_tokens, dim, generator=gen, device=gpu).to(dtype)
     dy, dw_rows = ops.moe_row_grad(dout, perm.sorted_token, perm.sorted_w, y_unw)
     dg, du = ops.moe_gemm_dgrad_down(dy, perm.tiles, td, gu, E)
     dx_perm = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim)
@@ -86,9 +99,11 @@ def test_backward_kernels(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew):
 
     # row gradient: dy bit-exact (one bf16 product), dw within summation order
     dp = dout[perm.sorted_token.long()]
-    assert torch.equal(dy, (dp.float() * perm.sorted_w.float().unsqueeze(-1)).to(BF))
+    assert torch.equal(dy, (dp.float() * perm.sorted_w.float().unsqueeze(-1)).to(dtype))
     dw_ref = (dp * y_unw).float().sum(-1)
-    torch.testing.assert_close(dw_rows.float(), dw_ref, rtol=2e-2, atol=1e-2 * dw_ref.abs().max().item())
+    fp32 = dtype == torch.float32
+    torch.testing.assert_close(dw_rows.float(), dw_ref, rtol=1e-4 if fp32 else 2e-2,
+                               atol=(1e-5 if fp32 else 1e-2) * dw_ref.abs().max().item())
 
     offs = perm.expert_offsets.tolist()
     live = [e for e in range(E) if offs[e + 1] > offs[e]]
@@ -101,17 +116,18 @@ def test_backward_kernels(gpu, n_tok, n_exp, top_k, dim, dim_ffn, skew):
         _close(u[a:b], xe @ wu[e].float().T, f"e{e} u")
         _close(y_unw[a:b], h[a:b].float() @ wd[e].float().T, f"e{e} y")
         # dgrad of down with the SwiGLU backward (rounding points of autograd over mlp.py:23)
-        dh = (dy[a:b].float() @ wd[e].float()).to(BF).float()
+        dh = (dy[a:b].float() @ wd[e].float()).to(dtype).float()
         gf, uf = g[a:b].float(), u[a:b].float()
         s = torch.sigmoid(gf)
-        act = F.silu(gf).to(BF).float()
+        act = F.silu(gf).to(dtype).float()
         du_ref = dh * act
-        dg_ref = (dh * uf).to(BF).float() * (s * (1 + gf * (1 - s)))
+        dg_ref = (dh * uf).to(dtype).float() * (s * (1 + gf * (1 - s)))
         _close(du[a:b], du_ref, f"e{e} du")
         _close(dg[a:b], dg_ref, f"e{e} dg")
         # dgrad of gate/up on the kernel's own dg, du: each linear's input
         # gradient rounded, then their sum (autograd's accumulation)
-        dx_ref = (dg[a:b].float() @ wg[e].float()).to(BF).float() + (du[a:b].float() @ wu[e].float()).to(BF).float()
+        dx_ref = ((dg[a:b].float() @ wg[e].float()).to(dtype).float()
+                  + (du[a:b].float() @ wu[e].float()).to(dtype).float())
         _close(dx_perm[a:b], dx_ref, f"e{e} dx_perm")
         # weight gradients
         _close(dwd[e], dy[a:b].float().T @ h[a:b].float(), f"e{e} dW_down")

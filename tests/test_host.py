@@ -185,23 +185,27 @@ def test_abi_rejects_bad_arguments_with_message():
     assert rc == -1 and "dim % 256" in loader.last_error()
     rc = lib.astrai_moe_pack_down(8, 1, 256, 64, 32, None)
     assert rc == -1 and "16-byte aligned" in loader.last_error()
-    # training / backward entry points (bf16, matrix-core shapes, 256-row tile lists)
-    rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 0, 4, 2, 256, 128, 256, 1, 1, None)
-    assert rc == -1 and "bf16 only" in loader.last_error()
+    # training / backward entry points: every call below is refused on the host
+    # (the dummy pointers are never dereferenced); fp32 and general shapes are
+    # accepted, so they do not appear here with dummy pointers
+    rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 7, 4, 2, 256, 128, 256, 1, 1, None)
+    assert rc == -1 and "dtype" in loader.last_error()
     rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 1, 4, 2, 256, 128, 32, 1, 1, None)
     assert rc == -1 and "256-row tile list" in loader.last_error()
-    rc = lib.astrai_moe_gemm_down_train(1, 1, 7, 1, 1, 1, 4, 2, 128, 200, 256, 1, 1, None)
-    assert rc == -1 and "dim % 256" in loader.last_error()
+    rc = lib.astrai_moe_gemm_down_train(1, 1, 7, 1, 1, 1, 4, 2, 0, 256, 256, 1, 1, None)
+    assert rc == -1 and "dims" in loader.last_error()
     rc = lib.astrai_moe_gemm_dgrad_down(1, 1, 7, 1, None, 1, 4, 2, 256, 128, 256, 1, 1, None)
     assert rc == -1 and "null" in loader.last_error()
-    rc = lib.astrai_moe_gemm_dgrad_gate_up(1, 1, 1, 7, 1, 1, 1, 4, 2, 100, 256, 256, 1, None)
-    assert rc == -1 and "dim_ffn % 128" in loader.last_error()
-    rc = lib.astrai_moe_row_grad(1, 1, 1, 1, 1, 4, 12, 1, 1, None)
-    assert rc == -1 and "dim % 8" in loader.last_error()
-    rc = lib.astrai_moe_gemm_wgrad(16, 16, 16, 1, 4, 2, 12, 16, 16, None)
-    assert rc == -1 and "m % 8" in loader.last_error()
-    rc = lib.astrai_moe_gemm_wgrad(8, 16, 16, 1, 4, 2, 16, 16, 16, None)
-    assert rc == -1 and "16-byte aligned" in loader.last_error()
+    rc = lib.astrai_moe_gemm_dgrad_gate_up(1, 1, 1, 7, 1, 1, 1, 4, 2, 128, 256, 64, 1, None)
+    assert rc == -1 and "256-row tile list" in loader.last_error()
+    rc = lib.astrai_moe_row_grad(1, 1, 1, 1, 1, 4, 0, 1, 1, None)
+    assert rc == -1 and "dim must be" in loader.last_error()
+    rc = lib.astrai_moe_row_grad(1, 1, 1, 1, 5, 4, 16, 1, 1, None)
+    assert rc == -1 and "dtype" in loader.last_error()
+    rc = lib.astrai_moe_gemm_wgrad(16, 16, 16, 1, 4, 2, 0, 16, 16, None)
+    assert rc == -1 and "m and n" in loader.last_error()
+    rc = lib.astrai_moe_gemm_wgrad(16, 16, None, 1, 4, 2, 16, 16, 16, None)
+    assert rc == -1 and "null" in loader.last_error()
     assert lib.astrai_moe_gemm_wgrad(None, None, None, 1, 0, 2, 16, 16, None, None) == 0
     # Empty inputs are a valid no-op.
     assert lib.astrai_moe_route(None, 1, 0, 8, 2, None, None, None, None) == 0
