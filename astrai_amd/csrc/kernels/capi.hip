@@ -40,18 +40,20 @@ extern "C" const char* astrai_moe_last_error(void) { return g_last_error; }
 // Row-tile policy. The bf16 matrix-core kernels need K % 64 == 0 for both
 // GEMMs, dim_ffn % 128 == 0 (gate/up column tiles) and dim % 256 == 0 (down
 // column tiles); other shapes and fp32 use the general kernel with 64-row
-// tiles. Among matrix-core tiles (measured on MI355X, both GEMMs):
+// tiles. Among matrix-core tiles (measured on MI355X, both GEMMs, one process,
+// outputs bit-identical across heights):
 // - routed experts, by average rows per expert: 32-row tiles below 24 rows
-//   (decode: the work is streaming the experts' weights; 32 and 64 tie at 16),
-//   64-row tiles below 96 (each tile streams its expert's weights, 256-row
-//   tiles would mostly compute padding: 64-row tiles are up to 23 % faster
-//   than either neighbour at 24-64 rows), 256-row tiles from 96 (the two cross
-//   at 80 rows for E128/F1536 and E64/F1408, at 120 for E8/F14336);
+//   (decode: the work is streaming the experts' weights), 64-row tiles below
+//   48, 128-row tiles below 128 (one tile per expert reads its weights once;
+//   at 64 rows per expert 10 % faster than 64-row tiles, at 80 rows 17 %),
+//   256-row tiles from 128 (crossing between 112 and 160 rows for E128/F1536,
+//   E64/F1408 and E8/F14336);
 // - one dense MLP over all tokens (n_experts = top_k = 1, the shared
-//   experts): all row tiles read the same weights, so extra 64-row tiles cost
-//   little until the launch has about one 256-row work unit per CU; 256-row
-//   tiles win from there (T * (dim_ffn / 128 + dim / 256) >= 256 * 256: T 512
-//   at D4096/F14336, 1490 at D7168/F2048, 2185 at D2048/F2816).
+//   experts): all row tiles read the same weights, so the tile height trades
+//   launch occupancy against per-tile efficiency. With u = T * (dim_ffn / 128
+//   + dim / 256) (256-row work units x 256): 64-row tiles below one work unit
+//   per CU (u < 65536), 128-row tiles up to 2.25 per CU, 256-row tiles beyond
+//   (D2048/F2816, D4096/F14336, D7168/F2048 at 64-4096 tokens).
 extern "C" int astrai_moe_select_block_m(int64_t n_tokens, int n_experts,
                                          int top_k, int64_t dim,
                                          int64_t dim_ffn, int dtype) {
@@ -66,10 +68,12 @@ extern "C" int astrai_moe_select_block_m(int64_t n_tokens, int n_experts,
   if (!mfma_shapes) return 64;
   if (n_experts == 1 && top_k == 1) {
     if (n_tokens < 96) return kMfmaSmallBM;
-    const int64_t col_tiles = dim_ffn / 128 + dim / 256;  // gate/up + down column tiles per row tile
-    return n_tokens * col_tiles >= 256 * 256 ? kMfmaBigBM : kMfmaMidBM;
+    const int64_t units = n_tokens * (dim_ffn / 128 + dim / 256);  // gate/up + down column tiles per row
+    if (units < 256 * 256) return kMfmaMidBM;
+    return units * 4 < 9 * 256 * 256 ? kMfmaMid2BM : kMfmaBigBM;
   }
   const int64_t rows_per_expert = n_tokens * top_k / n_experts;
   if (rows_per_expert < 24) return kMfmaSmallBM;
-  return rows_per_expert < 96 ? kMfmaMidBM : kMfmaBigBM;
+  if (rows_per_expert < 48) return kMfmaMidBM;
+  return rows_per_expert < 128 ? kMfmaMid2BM : kMfmaBigBM;
 }

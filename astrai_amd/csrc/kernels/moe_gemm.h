@@ -16,6 +16,9 @@ constexpr int kMfmaSmallBM = 32;
 // expert reads its weights once, where 32-row tiles would stream them twice or
 // more and 256-row tiles would compute mostly padding.
 constexpr int kMfmaMidBM = 64;
+// Loads of up to about 128 rows per expert: one 128-row tile per expert reads
+// its weights once where two 64-row tiles would stream them twice.
+constexpr int kMfmaMid2BM = 128;
 
 // Shape constraints of the bf16 kernels: K a multiple of 64, the output
 // columns a multiple of the column tile, 16-byte aligned operands.

@@ -213,17 +213,22 @@ __device__ __forceinline__ void store_tile(f32x4_t (&acc)[WM / 16][WN / 16], cha
       }
       *reinterpret_cast<bf16x4_t*>(stage + row_l * OROW + (j * 16 + col_l) * 2) = o;
     }
+    // the 16 staged rows go out as 16 x SEGS pieces of 16 bytes, lane by lane
+    // (one pass covers 64 pieces; narrow waves leave lanes idle)
     constexpr int SEGS = OUTC * 2 / 16;
-    constexpr int RPP = 64 / SEGS;
+    constexpr int PIECES = 16 * SEGS;
     wait_lds();
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int p = 0; p < 16 / RPP; ++p) {
-      const int m = p * RPP + el / SEGS;
-      const int seg = el % SEGS;
+    for (int p = 0; p < (PIECES + 63) / 64; ++p) {
+      const int idx = p * 64 + el;
+      const int m = idx / SEGS;
+      const int seg = idx % SEGS;
       const int gm = wm * WM + i * 16 + m;
-      const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
-      if (gm < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gm) * N + n_base + seg * 8) = v;
+      if (idx < PIECES) {
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
+        if (gm < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gm) * N + n_base + seg * 8) = v;
+      }
     }
     wait_lds();
     __builtin_amdgcn_wave_barrier();
@@ -744,6 +749,10 @@ using SmallCfg = TileCfg<kMfmaSmallBM, 256, 4, 1, 4, 8>;
 // rows of waves), three stages in flight: 3 x 40 KB of stages + the waves'
 // epilogue slices fit the 160 KB of LDS.
 using MidCfg = TileCfg<kMfmaMidBM, 256, 3, 2, 4, 8>;
+// 128-row tiles: 128 x 256 outputs, 8 waves side by side (128 x 32 each, so
+// the down epilogue's per-wave 16-row slices stay small), three 48 KB stages
+// in flight: 144 KB of stages + 10 KB of epilogue slices.
+using Mid2Cfg = TileCfg<kMfmaMid2BM, 256, 3, 1, 8, 8>;
 static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfmaBigBM, "prefill tile height");
 
 template <bool kGateUp, bool kPacked, bool kSave = false, bool kGather = false>
@@ -782,6 +791,8 @@ int gate_up_dispatch(const void* x_perm, const int32_t* tiles, int64_t capacity,
     return launch_stream<true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
+  if (block_m == kMfmaMid2BM)
+    return launch<Mid2Cfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
   return launch<SmallCfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
 }
 
@@ -792,6 +803,8 @@ int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const v
     return launch_stream<false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
+  if (block_m == kMfmaMid2BM)
+    return launch<Mid2Cfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
   return launch<SmallCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
 }
 
@@ -799,12 +812,14 @@ int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const v
 
 bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m, const void* a, const void* c) {
   // 32-bit DMA offsets: a tile spans at most 256 rows of K * 2 bytes
-  return (block_m == kMfmaBigBM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) && dim % kBK == 0 &&
+  return (block_m == kMfmaBigBM || block_m == kMfmaMid2BM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) &&
+         dim % kBK == 0 &&
          dim_ffn % 128 == 0 && dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m, const void* a, const void* c) {
-  return (block_m == kMfmaBigBM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) && dim_ffn % kBK == 0 &&
+  return (block_m == kMfmaBigBM || block_m == kMfmaMid2BM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) &&
+         dim_ffn % kBK == 0 &&
          dim % 256 == 0 && dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
@@ -845,6 +860,9 @@ int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token, const
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
                                              sorted_token);
+  if (block_m == kMfmaMid2BM)
+    return launch<Mid2Cfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
+                                              sorted_token);
   return launch<SmallCfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
                                              sorted_token);
 }

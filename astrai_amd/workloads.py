@@ -77,7 +77,7 @@ WORKLOADS = {
         Workload("moe_bf16_d4096_f14336_e8_k2_t16384", torch.bfloat16, 8, 2048, 4096, 14336, 8, 2, seed=3),
         Workload("moe_bf16_d4096_f1536_e128_k8_t64", torch.bfloat16, 64, 1, 4096, 1536, 128, 8, seed=4,
                  router_std=1.0 / 64.0),
-        # batched decode / chunked prefill: 64 rows per expert on average (64-row tiles)
+        # batched decode / chunked prefill: 64 rows per expert on average (128-row tiles)
         Workload("moe_bf16_d4096_f1536_e128_k8_t1024", torch.bfloat16, 1024, 1, 4096, 1536, 128, 8, seed=5,
                  router_std=1.0 / 64.0),
     ]

@@ -312,7 +312,7 @@ def main():
     traffic = MEASURED_TRAFFIC_BYTES.get(name)
     block_m = ops.select_block_m(T, w.n_experts, w.top_k, w.dim, w.dim_ffn, w.dtype)
     timing = f"HIP events on the launch stream around each of its {args.steps} launches in the layer forward"
-    if bf16 and block_m in (32, 64):
+    if bf16 and block_m in (32, 64, 128):
         # decode- and mid-sized loads: the gate/up kernel streams the routed experts' weights
         gu_bytes = n_active * 2.0 * w.dim * w.dim_ffn * s + rows * w.dim * s + rows * w.dim_ffn * s
         gbs = gu_bytes / t_roof / 1e9

@@ -190,7 +190,7 @@ int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
  * of the permuted input is x[sorted_token[r]], so the permutation need not
  * copy x (astrai_moe_permute with x_perm = NULL). Same results as
  * astrai_moe_gemm_gate_up on the copied rows (bit-identical). bf16 and the
- * matrix-core block sizes (32, 64 or 256) only; x under 4 GiB.
+ * matrix-core block sizes (32, 64, 128 or 256) only; x under 4 GiB.
  *
  *   x             [n_tokens, dim]   bf16
  *   sorted_token  [n_rows]          int32, from astrai_moe_permute
@@ -254,7 +254,7 @@ int astrai_moe_pack_down(const void* w_down, int dtype, int64_t dim,
  * The grouped GEMMs reading packed weights: same arguments, results and
  * rounding as astrai_moe_gemm_gate_up / astrai_moe_gemm_down (bit-identical),
  * with the weight tables pointing at packed copies. bf16 and the matrix-core
- * block sizes only (block_m from astrai_moe_select_block_m being 32, 64 or 256);
+ * block sizes only (block_m from astrai_moe_select_block_m being 32, 64, 128 or 256);
  * other cases return ASTRAI_MOE_EINVAL.
  */
 int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t* tiles,

@@ -196,7 +196,7 @@ def test_gate_up_gather_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
     experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=14)
     bm = ops.select_block_m(n_tok, n_exp, top_k, dim, dim_ffn, dtype)
-    assert bm in (32, 64, 256)
+    assert bm in (32, 64, 128, 256)
     perm = ops.moe_permute(route, x, n_exp, bm)
     idx = ops.moe_permute(route, x, n_exp, bm, copy_rows=False)
     assert idx.x_perm is None
@@ -273,6 +273,7 @@ def test_long_k_rows(gpu, n_tok, n_exp, top_k, dim, dim_ffn, block_m):
     (300, 16, 4, 512, 256),  # 32-row tiles
     (64, 128, 8, 4096, 1536),  # decode-sized loads over many experts
     (16384, 4, 2, 256, 128),  # one column tile per expert for gate/up
+    (1024, 128, 8, 4096, 1536),  # 128-row tiles (64 rows per expert)
 ])
 def test_packed_gemms_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     dtype = torch.bfloat16
@@ -309,11 +310,13 @@ def test_packed_gemms_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     (700, 16, 4, 2048, 768),  # ragged row tiles
     (1, 8, 2, 1024, 1024),  # one token
     (512, 8, 1, 1024, 512),  # 64 rows per expert: one 64-row tile each
+    (1024, 8, 1, 1024, 512),  # 128 rows per expert: one 128-row tile each
+    (900, 16, 3, 2048, 768),  # ~170 rows per expert: two 128-row tiles, ragged
 ])
-@pytest.mark.parametrize("bm", [32, 64])
+@pytest.mark.parametrize("bm", [32, 64, 128])
 def test_decode_gemms_row_strided_packed_gathered_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn, bm):
-    # 32- and 64-row tiles: row-strided, packed and gathered operands give
-    # equal bits, the two tile heights give equal bits (the same per-wave MFMA
+    # 32-, 64- and 128-row tiles: row-strided, packed and gathered operands
+    # give equal bits, the tile heights give equal bits (the same per-wave MFMA
     # sequence over K), and every expert's rows match torch
     dtype = torch.bfloat16
     route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=21)
@@ -394,7 +397,8 @@ def test_combine_bit_exact(gpu, n_tok, n_exp, top_k, dim, n_shared, dtype):
 @pytest.mark.parametrize("n_tok,dim,dim_ffn,dtype", [
     (1, 256, 128, torch.bfloat16),      # 32-row tiles
     (200, 256, 256, torch.bfloat16),    # 64-row tiles
-    (3000, 2048, 2048, torch.bfloat16), # 256-row tiles
+    (3000, 2048, 2048, torch.bfloat16), # 128-row tiles
+    (8192, 2048, 2048, torch.bfloat16), # 256-row tiles
     (37, 40, 24, torch.bfloat16),       # general kernel
     (129, 64, 96, torch.float32),       # general kernel, fp32
 ])

@@ -221,7 +221,7 @@ def test_tile_list_len_bounds_the_tile_count():
         n_exp = rnd.randint(1, 64)
         k = rnd.randint(1, min(8, n_exp))
         n_tok = rnd.randint(0, 5000)
-        bm = rnd.choice([32, 64, 256])
+        bm = rnd.choice([32, 64, 128, 256])
         rows = n_tok * k
         cuts = sorted(rnd.randint(0, rows) for _ in range(n_exp - 1))
         counts = [b - a for a, b in zip([0] + cuts, cuts + [rows])]
@@ -236,20 +236,28 @@ def test_block_m_policy():
     assert ops.select_block_m(64, 128, 8, 4096, 1536, bf) == 32
     assert ops.select_block_m(1024, 8, 2, 512, 1024, torch.float32) == 64  # the general kernel's tiles
     assert ops.select_block_m(100, 4, 2, 8, 16, bf) == 64  # shapes the MFMA kernels do not tile
-    # routed, by average rows per expert: 32-row tiles below 24, 64-row tiles below 96, then 256
+    # routed, by average rows per expert: 32-row tiles below 24, 64 below 48, 128 below 128, then 256
     assert ops.select_block_m(368, 128, 8, 4096, 1536, bf) == 32  # 23 rows per expert
     assert ops.select_block_m(384, 128, 8, 4096, 1536, bf) == 64  # 24
-    assert ops.select_block_m(1520, 128, 8, 4096, 1536, bf) == 64  # 95
-    assert ops.select_block_m(1536, 128, 8, 4096, 1536, bf) == 256  # 96
-    assert ops.select_block_m(383, 8, 2, 4096, 14336, bf) == 64
-    assert ops.select_block_m(384, 8, 2, 4096, 14336, bf) == 256
-    # one dense MLP (shared experts): 32 below 96 tokens, 256 once T * (F/128 + D/256) >= 65536
+    assert ops.select_block_m(767, 128, 8, 4096, 1536, bf) == 64  # 47
+    assert ops.select_block_m(768, 128, 8, 4096, 1536, bf) == 128  # 48
+    assert ops.select_block_m(1024, 128, 8, 4096, 1536, bf) == 128  # 64: the mid-sized batch workload
+    assert ops.select_block_m(2047, 128, 8, 4096, 1536, bf) == 128  # 127
+    assert ops.select_block_m(2048, 128, 8, 4096, 1536, bf) == 256  # 128
+    assert ops.select_block_m(511, 8, 2, 4096, 14336, bf) == 128
+    assert ops.select_block_m(512, 8, 2, 4096, 14336, bf) == 256
+    assert ops.select_block_m(8192, 64, 6, 2048, 1408, bf) == 256  # the fine-grained workload (768 rows)
+    # one dense MLP (shared experts): 32 below 96 tokens; with u = T * (F/128 + D/256): 64-row tiles
+    # below u = 65536, 128 below 2.25 * 65536, then 256
     assert ops.select_block_m(95, 1, 1, 2048, 2816, bf) == 32
     assert ops.select_block_m(96, 1, 1, 2048, 2816, bf) == 64
     assert ops.select_block_m(2184, 1, 1, 2048, 2816, bf) == 64  # 30 column tiles per row tile
-    assert ops.select_block_m(2185, 1, 1, 2048, 2816, bf) == 256
+    assert ops.select_block_m(2185, 1, 1, 2048, 2816, bf) == 128
+    assert ops.select_block_m(4915, 1, 1, 2048, 2816, bf) == 128
+    assert ops.select_block_m(4916, 1, 1, 2048, 2816, bf) == 256
     assert ops.select_block_m(511, 1, 1, 4096, 14336, bf) == 64  # 128 column tiles per row tile
-    assert ops.select_block_m(512, 1, 1, 4096, 14336, bf) == 256
+    assert ops.select_block_m(512, 1, 1, 4096, 14336, bf) == 128
+    assert ops.select_block_m(1152, 1, 1, 4096, 14336, bf) == 256
     assert ops.select_block_m(16384, 1, 1, 2048, 2816, bf) == 256
 
 
@@ -357,7 +365,7 @@ def test_tile_list_height_is_checked_before_any_launch(monkeypatch):
     n_exp, dim, dim_ffn, bf = 4, 256, 128, torch.bfloat16
     x = torch.zeros(64, dim, dtype=bf)
     good = torch.zeros(n_exp, dtype=torch.int64)
-    for built in (32, 64, 256):
+    for built in (32, 64, 128, 256):
         tiles = ops._tag_tiles(torch.zeros(64, dtype=torch.int32), built)
         for name, call in _table_wrappers(x, tiles, n_exp, dim, dim_ffn).items():
             runs_at = 256 if name.endswith("train") or name.startswith("dgrad") else 32
