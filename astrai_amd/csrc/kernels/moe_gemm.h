@@ -61,6 +61,24 @@ int launch_mfma_down_save(const void* h, const int32_t* tiles,
                           const void* sorted_w, int64_t dim_ffn, int64_t dim,
                           void* y, void* y_unweighted, hipStream_t s);
 
+// fp32 on the matrix cores (moe_gemm_mfma_f32.hip), 64-row tile lists, K a
+// multiple of 32, output columns a multiple of 32 (gate/up) or 64 (down),
+// 16-byte aligned operands. A non-null gu / y_unweighted selects the training
+// forward, which also stores the gate and up projections (blocked layout of
+// gu_index) or the output before the routing weight.
+bool mfma_f32_supported(int64_t k, int64_t n, bool gate_up, int block_m,
+                        const void* a, const void* c, const void* s0);
+int launch_mfma_f32_gate_up(const void* x_perm, const int32_t* tiles,
+                            int64_t capacity, const void* const* w_gate,
+                            const void* const* w_up, int64_t n_rows,
+                            int n_experts, int64_t dim, int64_t dim_ffn,
+                            void* h, void* gu, hipStream_t s);
+int launch_mfma_f32_down(const void* h, const int32_t* tiles, int64_t capacity,
+                         const void* const* w_down, const void* sorted_w,
+                         int64_t n_rows, int n_experts, int64_t dim_ffn,
+                         int64_t dim, void* y, void* y_unweighted,
+                         hipStream_t s);
+
 // Backward (moe_gemm_bwd.hip), bf16, 256-row tile lists:
 // dy = dout[sorted_token] * sorted_w and dw_rows = sum(dout[tok] * y) per row;
 int launch_row_grad(const void* dout, const int32_t* sorted_token,

@@ -18,9 +18,11 @@
 // Kernels:
 //   * gemm_mfma_* (moe_gemm_mfma.hip): bf16 on CDNA4 matrix cores, used when
 //     the shapes meet its tiling constraints.
+//   * gemm_f32_mfma_kernel (moe_gemm_mfma_f32.hip): fp32 on CDNA4 matrix
+//     cores (v_mfma_f32_16x16x4_f32), 64-row tiles, K a multiple of 32.
 //   * gemm_generic_kernel (here): any shape, fp32 or bf16, fp32 FMA; 64x64
-//     output tiles walked over the row tile in 64-row steps. Used for fp32 and
-//     for shapes the MFMA kernel does not tile.
+//     output tiles walked over the row tile in 64-row steps. Used for the
+//     shapes neither matrix-core kernel tiles.
 #include "moe_common.h"
 #include "moe_gemm.h"
 
@@ -194,6 +196,9 @@ extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
     return launch_generic<bf16_t, true>(x_perm, tiles, capacity, w_gate, w_up,
                                         nullptr, dim, dim_ffn, h, s);
   }
+  if (mfma_f32_supported(dim, dim_ffn, true, block_m, x_perm, h, nullptr))
+    return launch_mfma_f32_gate_up(x_perm, tiles, capacity, w_gate, w_up, n_rows, n_experts, dim, dim_ffn, h,
+                                   nullptr, s);
   return launch_generic<float, true>(x_perm, tiles, capacity, w_gate, w_up,
                                      nullptr, dim, dim_ffn, h, s);
 }
@@ -242,6 +247,9 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
     return launch_generic<bf16_t, false>(h, tiles, capacity, w_down, nullptr,
                                          sorted_w, dim_ffn, dim, y, s);
   }
+  if (mfma_f32_supported(dim_ffn, dim, false, block_m, h, y, nullptr))
+    return launch_mfma_f32_down(h, tiles, capacity, w_down, sorted_w, n_rows, n_experts, dim_ffn, dim, y, nullptr,
+                                s);
   return launch_generic<float, false>(h, tiles, capacity, w_down, nullptr,
                                       sorted_w, dim_ffn, dim, y, s);
 }
@@ -353,6 +361,8 @@ extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* 
   if (dtype == ASTRAI_MOE_BF16)
     return launch_generic<bf16_t, true, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
                                               gu);
+  if (mfma_f32_supported(dim, dim_ffn, true, block_m, x_perm, h, gu))
+    return launch_mfma_f32_gate_up(x_perm, tiles, capacity, w_gate, w_up, n_rows, n_experts, dim, dim_ffn, h, gu, s);
   return launch_generic<float, true, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, gu);
 }
 
@@ -376,6 +386,9 @@ extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, i
   if (dtype == ASTRAI_MOE_BF16)
     return launch_generic<bf16_t, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
                                                y_unweighted);
+  if (mfma_f32_supported(dim_ffn, dim, false, block_m, h, y, y_unweighted))
+    return launch_mfma_f32_down(h, tiles, capacity, w_down, sorted_w, n_rows, n_experts, dim_ffn, dim, y,
+                                y_unweighted, s);
   return launch_generic<float, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
                                             y_unweighted);
 }

@@ -143,7 +143,8 @@ def expert_weight_table(weights: Sequence[torch.Tensor], shape: tuple[int, int])
     """Device array of the experts' weight pointers (int64), for the GEMMs.
 
     Every weight must be a contiguous ``[out, in] == shape`` tensor on one
-    device with one dtype; the kernels read them in place.
+    device with one dtype, starting on a 16-byte boundary when its rows are a
+    multiple of 16 bytes; the kernels read them in place.
     """
     if len(weights) == 0:
         raise ValueError("no expert weights")
@@ -154,6 +155,9 @@ def expert_weight_table(weights: Sequence[torch.Tensor], shape: tuple[int, int])
             raise ValueError(f"expert weight {i} has shape {tuple(w.shape)}, expected {tuple(shape)}")
         if w.device != dev or w.dtype != dt:
             raise ValueError("expert weights must share one device and dtype")
+        # rows of a multiple of 16 bytes are read with 16-byte vector loads
+        if (w.shape[1] * w.element_size()) % 16 == 0 and w.data_ptr() % 16 != 0:
+            raise ValueError(f"expert weight {i} must start on a 16-byte boundary (its rows are read 16 bytes at a time)")
     return torch.tensor([w.data_ptr() for w in weights], dtype=torch.int64).to(dev)
 
 
@@ -313,6 +317,14 @@ def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, so
         "moe_gemm_down",
     )
     return y
+
+
+def f32_matrix_cores(dim: int, dim_ffn: int, block_m: int, dtype: torch.dtype) -> bool:
+    """Whether both fp32 GEMMs of this shape run on the matrix cores
+    (``gemm_f32_mfma_kernel``: 64-row tiles, dim and dim_ffn multiples of 32,
+    dim a multiple of 64 for the down GEMM's column tiles)."""
+    return (dtype == torch.float32 and block_m == 64 and dim % 64 == 0 and dim_ffn % 32 == 0
+            and 0 < dim <= 1 << 22 and 0 < dim_ffn <= 1 << 22)
 
 
 def packed_supported(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:

@@ -180,7 +180,7 @@ def cpu_baseline(layer, x, w, target_s: float) -> dict:
             n = int(min(x_all.shape[0], max(n_warm, 0.2 * target_s / per_tok)))
         n = int(min(x_all.shape[0], max(n_warm, target_s / per_tok)))
         # a workload shorter than the target is timed over repeated passes
-        reps = max(1, min(8, round(target_s / (n * per_tok))))
+        reps = max(1, min(2000, round(target_s / (n * per_tok))))
         xs = x_all[:n].cpu()
         t0 = time.perf_counter()
         for _ in range(reps):
@@ -322,8 +322,13 @@ def main():
                     "timing": timing}
     else:
         achieved = flops_gate_up / t_roof / 1e12
-        roofline = {"kernel": (("gemm_stream_kernel<gate_up, gather>" if gathered else "gemm_stream_kernel<gate_up>")
-                               if bf16 else "gemm_generic_kernel<gate_up>"),
+        if bf16:
+            kname = "gemm_stream_kernel<gate_up, gather>" if gathered else "gemm_stream_kernel<gate_up>"
+        elif ops.f32_matrix_cores(w.dim, w.dim_ffn, block_m, w.dtype):
+            kname = "gemm_f32_mfma_kernel<gate_up>"
+        else:
+            kname = "gemm_generic_kernel<gate_up>"
+        roofline = {"kernel": kname,
                     "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
                     "traffic": traffic, "algorithmic_flops_per_launch": flops_gate_up, "kernel_ms": t_gu * 1e3,
                     "timing": timing}

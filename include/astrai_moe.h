@@ -178,6 +178,13 @@ int astrai_moe_dense_tiles(int64_t n_rows, int block_m, int32_t* tiles,
  *   tiles   tile list from astrai_moe_permute (same block_m)
  *   w_gate, w_up  device arrays of n_experts pointers, each [dim_ffn, dim]
  *   h       [n_rows, dim_ffn]       dtype
+ *
+ * Kernels (both GEMMs): bf16 runs on the matrix cores when K is a multiple
+ * of 64 and the output columns of the column tiles (dim_ffn % 128, dim % 256);
+ * fp32 runs on the matrix cores (v_mfma_f32_16x16x4_f32) with block_m = 64,
+ * K a multiple of 32 and dim_ffn % 32 == 0 (gate/up) or dim % 64 == 0 (down);
+ * every other case on a general fp32-FMA kernel. Weights whose rows are a
+ * multiple of 16 bytes must start on a 16-byte boundary.
  */
 int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
                             int64_t tiles_len, const void* const* w_gate,
@@ -295,7 +302,9 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
  * kernels, at autograd's rounding points (identities in fp32): on the matrix
  * cores for bf16 with dim % 256 == 0 and dim_ffn % 128 == 0 (tile lists built
  * with block_m = 256), on the general-shape kernels for every other shape and
- * for fp32 (any block_m). Per expert e with permuted rows R_e:
+ * for fp32 (any block_m; the fp32 training forward takes the fp32 matrix-core
+ * GEMMs where astrai_moe_gemm_gate_up / _down would). Per expert e with
+ * permuted rows R_e:
  *
  *   forward   g = x W_gate^T, u = x W_up^T, h = u * silu(g), y = h W_down^T,
  *             out = sum over slots of y * w                    (mlp.py:22-24, :97-98)

@@ -146,7 +146,11 @@ GEMM_CASES = [
     # one 64-K step per tile, several tiles per workgroup: every step is a
     # tile's last and prefetches the next tile's first fragments
     (16384, 4, 2, 64, 1024, torch.bfloat16),
-    (1024, 8, 2, 512, 1024, torch.float32),
+    # fp32: matrix-core kernel (64-row tiles, K % 32 == 0) with each column-tile width, and the general kernel
+    (1024, 8, 2, 512, 1024, torch.float32),  # gate/up 128-wide tiles, down 64-wide
+    (4096, 16, 4, 1024, 512, torch.float32),  # 256-wide tiles for both
+    (300, 16, 4, 128, 96, torch.float32),  # gate/up 64-wide (96 columns), partial row tiles, skewed experts
+    (200, 4, 2, 32, 64, torch.float32),  # gate/up one K step; down 32 columns: general kernel
     (100, 5, 3, 36, 20, torch.float32),
 ]
 
