@@ -38,10 +38,10 @@ extern "C" int astrai_moe_abi_version(void) { return ASTRAI_MOE_ABI_VERSION; }
 extern "C" const char* astrai_moe_last_error(void) { return g_last_error; }
 
 // Row-tile policy. The bf16 matrix-core kernels need K % 64 == 0 for both
-// GEMMs, dim_ffn % 128 == 0 (gate/up column tiles) and dim % 256 == 0 (down
-// column tiles); other shapes and fp32 use the general kernel with 64-row
-// tiles. Among matrix-core tiles (measured on MI355X, both GEMMs, one process,
-// outputs bit-identical across heights):
+// GEMMs (dim and dim_ffn multiples of 64); other shapes and fp32 use 64-row
+// tiles (the fp32 matrix-core kernel's and the general kernel's). Among
+// matrix-core tiles (measured on MI355X, both GEMMs, one process, outputs
+// bit-identical across heights):
 // - routed experts, by average rows per expert: 32-row tiles below 24 rows
 //   (decode: the work is streaming the experts' weights), 64-row tiles below
 //   48, 128-row tiles below 128 (one tile per expert reads its weights once;
@@ -62,13 +62,13 @@ extern "C" int astrai_moe_select_block_m(int64_t n_tokens, int n_experts,
     return fail(ASTRAI_MOE_EINVAL, "select_block_m: bad sizes");
   if (dtype != ASTRAI_MOE_BF16 && dtype != ASTRAI_MOE_F32)
     return fail(ASTRAI_MOE_EINVAL, "select_block_m: unsupported dtype %d", dtype);
-  const bool mfma_shapes = dtype == ASTRAI_MOE_BF16 && dim % 64 == 0 &&
-                           dim_ffn % 128 == 0 && dim % 256 == 0 &&
+  const bool mfma_shapes = dtype == ASTRAI_MOE_BF16 && dim % 64 == 0 && dim_ffn % 64 == 0 &&
                            dim <= (1ll << 22) && dim_ffn <= (1ll << 22);
   if (!mfma_shapes) return 64;
   if (n_experts == 1 && top_k == 1) {
     if (n_tokens < 96) return kMfmaSmallBM;
-    const int64_t units = n_tokens * (dim_ffn / 128 + dim / 256);  // gate/up + down column tiles per row
+    // gate/up + down column tiles per row
+    const int64_t units = n_tokens * (ceil_div(dim_ffn, 128) + ceil_div(dim, 256));
     if (units < 256 * 256) return kMfmaMidBM;
     return units * 4 < 9 * 256 * 256 ? kMfmaMid2BM : kMfmaBigBM;
   }

@@ -291,7 +291,8 @@ extern "C" int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t*
                         block_m, h);
   if (rc) return rc;
   ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_gate_up_packed: packed weights are bf16 only");
-  ASTRAI_REQUIRE(n_rows == 0 || mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h),
+  // packed weights come in whole 256-row tiles (128 gate + 128 up rows)
+  ASTRAI_REQUIRE(n_rows == 0 || (dim_ffn % 128 == 0 && mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h)),
                  "gemm_gate_up_packed: unsupported shape (dim %lld, dim_ffn %lld, block_m %d) or alignment",
                  (long long)dim, (long long)dim_ffn, block_m);
   if (n_rows == 0) return ASTRAI_MOE_OK;
@@ -310,7 +311,7 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
                         y);
   if (rc) return rc;
   ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_down_packed: packed weights are bf16 only");
-  ASTRAI_REQUIRE(n_rows == 0 || mfma_down_supported(dim_ffn, dim, block_m, h, y),
+  ASTRAI_REQUIRE(n_rows == 0 || (dim % 256 == 0 && mfma_down_supported(dim_ffn, dim, block_m, h, y)),
                  "gemm_down_packed: unsupported shape (dim_ffn %lld, dim %lld, block_m %d) or alignment",
                  (long long)dim_ffn, (long long)dim, block_m);
   if (n_rows == 0) return ASTRAI_MOE_OK;

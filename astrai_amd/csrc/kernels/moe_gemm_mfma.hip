@@ -91,12 +91,15 @@ struct TileSrc {
   const char* b_base0 = nullptr;
   const char* b_base1 = nullptr;
   int row0 = 0, rows = 0;
+  int b_rows = 0;  // weight rows of this column tile inside the matrix (per operand for gate/up)
   __device__ void setup(const int32_t* tiles, const bf16_t* A, const void* const* W0, const void* const* W1, int K,
-                        int mt, int nt) {
+                        int N, int mt, int nt) {
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int e = ti[0];
     row0 = ti[1];
     rows = min(BM, ti[2] - row0);
+    constexpr int kTileRows = kGateUp ? BN / 2 : BN;
+    b_rows = min(kTileRows, N - nt * kTileRows);
     a_base = reinterpret_cast<const char*>(kGather ? A : A + (int64_t)row0 * K);
     if constexpr (kPacked) {
       b_base0 = static_cast<const char*>(W0[e]) + (int64_t)nt * (K / kBK) * (BN * kRowBytes);
@@ -117,7 +120,9 @@ struct TileSrc {
   __device__ void dma_a_rows(const DmaLane& dl, uint32_t row_off, int q, char* lds) const {
     lds_dma_16(a_base + (row_off + dl.chunk(q)), lds);
   }
-  // 8-row group q of the B tile of K step kstep (up rows follow the gate rows)
+  // 8-row group q of the B tile of K step kstep (up rows follow the gate rows;
+  // in a partial last column tile, rows past the matrix re-read its last row,
+  // and the epilogue stores none of their columns)
   __device__ void dma_b(const DmaLane& dl, int lane, int kstep, int q, uint32_t k2, char* lds) const {
     if constexpr (kPacked) {
       lds_dma_16(b_base0 + ((uint32_t)kstep * (BN * kRowBytes) + (uint32_t)q * 1024 + (uint32_t)lane * 16), lds);
@@ -126,7 +131,7 @@ struct TileSrc {
       const int r0 = q * 8;
       const char* bb = (kGateUp && r0 >= BN / 2) ? b_base1 : b_base0;
       const int rq = (kGateUp && r0 >= BN / 2) ? r0 - BN / 2 : r0;
-      lds_dma_16(bb + ((uint32_t)(rq + dl.row) * k2 + dl.chunk(q)), lds);
+      lds_dma_16(bb + ((uint32_t)min(rq + dl.row, b_rows - 1) * k2 + dl.chunk(q)), lds);
     }
   }
 };
@@ -227,7 +232,8 @@ __device__ __forceinline__ void store_tile(f32x4_t (&acc)[WM / 16][WN / 16], cha
       const int gm = wm * WM + i * 16 + m;
       if (idx < PIECES) {
         const uint4 v = *reinterpret_cast<const uint4*>(stage + m * OROW + seg * 16);
-        if (gm < t_rows) *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gm) * N + n_base + seg * 8) = v;
+        if (gm < t_rows && n_base + seg * 8 < N)
+          *reinterpret_cast<uint4*>(C + (int64_t)(t_row0 + gm) * N + n_base + seg * 8) = v;
       }
     }
     wait_lds();
@@ -319,7 +325,7 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
         }
         if constexpr (kSave && kGateUp) {
           // g and u in the accumulator layout: row r, column c of h -> 2 (r N + c)
-          if (gm < t_rows) {
+          if (gm < t_rows && n_base + j * 16 + 4 * q < N) {
             bf16x8_t gu;
 #pragma unroll
             for (int r = 0; r < 4; ++r) gu[r] = (__bf16)acc[i][j][r], gu[4 + r] = (__bf16)acc[i][j + NJ][r];
@@ -328,7 +334,8 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
         }
       }
       transpose2(o);
-      if (gm < t_rows) {
+      // N is a multiple of 8: a lane's 8 columns are all inside the matrix or all past it
+      if (gm < t_rows && n_base + jp * 16 + 8 * q < N) {
         bf16x8_t v;
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = o[0][r], v[4 + r] = o[1][r];
@@ -351,18 +358,18 @@ struct StepCursor {
   bool live;
   TileSrc<BM, BN, kGateUp, kPacked, kGather> src;
   __device__ void start(const TileWalk<GM>& walk, int logical_, int mt_, int nt_, const int32_t* tiles,
-                        const bf16_t* A, const void* const* W0, const void* const* W1, int K) {
+                        const bf16_t* A, const void* const* W0, const void* const* W1, int K, int N) {
     logical = logical_, mt = mt_, nt = nt_, kt = 0, live = true;
     (void)walk;
-    src.setup(tiles, A, W0, W1, K, mt, nt);
+    src.setup(tiles, A, W0, W1, K, N, mt, nt);
   }
   __device__ void advance(const TileWalk<GM>& walk, const int32_t* tiles, const bf16_t* A, const void* const* W0,
-                          const void* const* W1, int K, int KT) {
+                          const void* const* W1, int K, int N, int KT) {
     if (++kt == KT) {
       kt = 0;
       logical = walk.seek(logical + walk.G, mt, nt);
       live = logical < walk.total;
-      if (live) src.setup(tiles, A, W0, W1, K, mt, nt);
+      if (live) src.setup(tiles, A, W0, W1, K, N, mt, nt);
     }
   }
 };
@@ -404,8 +411,8 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     auto load_rows = [&]() {
       if constexpr (kGather) grows.load(row_src, ca.src.row0, ca.src.rows, dw * Cfg::OPS, lane, k2);
     };
-    ca.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
-    cb.start(walk, logical, mt, nt, tiles, A, W0, W1, K);
+    ca.start(walk, logical, mt, nt, tiles, A, W0, W1, K, N);
+    cb.start(walk, logical, mt, nt, tiles, A, W0, W1, K, N);
     load_rows();
     auto issue_a = [&](int buf) {
       const DmaLane dl(lane, ca.kt);
@@ -418,7 +425,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
         else
           ca.src.dma_a(dl, q, k2, base + q * 1024);
       }
-      ca.advance(walk, tiles, A, W0, W1, K, KT);
+      ca.advance(walk, tiles, A, W0, W1, K, N, KT);
       if (ca.live && ca.kt == 0) load_rows();  // the next tile's rows
     };
     auto issue_b = [&](int buf) {
@@ -429,7 +436,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
         const int q = dw * Cfg::OPS + i;
         cb.src.dma_b(dl, lane, cb.kt, q, k2, base + q * 1024);
       }
-      cb.advance(walk, tiles, A, W0, W1, K, KT);
+      cb.advance(walk, tiles, A, W0, W1, K, N, KT);
     };
     // prologue in issue order B0, A0, B1, A1, B2 (as far as the steps exist)
     int a_iss = 0, b_iss = 0;
@@ -612,7 +619,7 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   TileSrc<Cfg::BM, Cfg::BN, kGateUp, kPacked, kGather> src;
   GatherRows<Cfg::A_PER_WAVE> grows;
   auto setup_tile = [&](int mt_, int nt_) {
-    src.setup(tiles, A, W0, W1, K, mt_, nt_);
+    src.setup(tiles, A, W0, W1, K, N, mt_, nt_);
     if constexpr (kGather) grows.load(row_src, src.row0, src.rows, wave * Cfg::A_PER_WAVE, lane, k2);
   };
   auto issue_stage = [&](int kstep, int buf) {
@@ -761,7 +768,7 @@ int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const v
                   void* S1 = nullptr, const int32_t* row_src = nullptr) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   using Cfg = StreamCfg<kGateUp>;
-  const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
+  const int64_t n_tiles_n = ceil_div(N, kGateUp ? Cfg::BN / 2 : Cfg::BN);  // the last may be partial
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
   hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked, kSave, kGather>), dim3((unsigned)grid),
@@ -775,7 +782,7 @@ template <typename Cfg, bool kGateUp, bool kPacked, bool kGather = false>
 int launch(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
            const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s, const int32_t* row_src = nullptr) {
   if (capacity == 0) return ASTRAI_MOE_OK;
-  const int64_t n_tiles_n = kGateUp ? N / (Cfg::BN / 2) : N / Cfg::BN;
+  const int64_t n_tiles_n = ceil_div(N, kGateUp ? Cfg::BN / 2 : Cfg::BN);  // the last may be partial
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
   hipLaunchKernelGGL((gemm_mfma_kernel<Cfg, kGateUp, kPacked, kGather>), dim3((unsigned)grid), dim3(Cfg::THREADS),
@@ -810,17 +817,19 @@ int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const v
 
 }  // namespace
 
+// K a multiple of the 64-K step; output columns a multiple of 8 (16-byte
+// stores; the last column tile may be partial). 32-bit DMA offsets: a tile
+// spans at most 256 rows of K * 2 bytes.
 bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m, const void* a, const void* c) {
-  // 32-bit DMA offsets: a tile spans at most 256 rows of K * 2 bytes
   return (block_m == kMfmaBigBM || block_m == kMfmaMid2BM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) &&
-         dim % kBK == 0 &&
-         dim_ffn % 128 == 0 && dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
+         dim > 0 && dim_ffn > 0 && dim % kBK == 0 && dim_ffn % 8 == 0 && dim <= (1ll << 22) &&
+         dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m, const void* a, const void* c) {
   return (block_m == kMfmaBigBM || block_m == kMfmaMid2BM || block_m == kMfmaMidBM || block_m == kMfmaSmallBM) &&
-         dim_ffn % kBK == 0 &&
-         dim % 256 == 0 && dim <= (1ll << 22) && dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
+         dim > 0 && dim_ffn > 0 && dim_ffn % kBK == 0 && dim % 8 == 0 && dim <= (1ll << 22) &&
+         dim_ffn <= (1ll << 22) && aligned16(a) && aligned16(c);
 }
 
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,

@@ -258,10 +258,18 @@ def _out_buffer(out: torch.Tensor | None, rows: int, cols: int, like: torch.Tens
     return out
 
 
+def matrix_core_supported(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
+    """Whether the bf16 forward GEMMs of this expert shape run on the matrix
+    cores (dim and dim_ffn multiples of 64; the last column tile may be
+    partial)."""
+    return (dtype == torch.bfloat16 and dim % 64 == 0 and dim_ffn % 64 == 0 and 0 < dim <= 1 << 22
+            and 0 < dim_ffn <= 1 << 22)
+
+
 def gather_supported(n_tokens: int, dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
     """Whether ``moe_gemm_gate_up_gather`` takes this problem (bf16, the
     matrix-core shapes, x under 4 GiB)."""
-    return packed_supported(dim, dim_ffn, dtype) and n_tokens * dim * 2 < 1 << 32
+    return matrix_core_supported(dim, dim_ffn, dtype) and n_tokens * dim * 2 < 1 << 32
 
 
 def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor,
@@ -329,7 +337,7 @@ def f32_matrix_cores(dim: int, dim_ffn: int, block_m: int, dtype: torch.dtype) -
 
 def packed_supported(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
     """Whether the packed-weight GEMMs take this expert shape (bf16, dim a
-    multiple of 256, dim_ffn a multiple of 128)."""
+    multiple of 256, dim_ffn a multiple of 128: whole column tiles)."""
     return (dtype == torch.bfloat16 and dim % 256 == 0 and dim_ffn % 128 == 0 and 0 < dim <= 1 << 22
             and 0 < dim_ffn <= 1 << 22)
 

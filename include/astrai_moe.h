@@ -179,8 +179,10 @@ int astrai_moe_dense_tiles(int64_t n_rows, int block_m, int32_t* tiles,
  *   w_gate, w_up  device arrays of n_experts pointers, each [dim_ffn, dim]
  *   h       [n_rows, dim_ffn]       dtype
  *
- * Kernels (both GEMMs): bf16 runs on the matrix cores when K is a multiple
- * of 64 and the output columns of the column tiles (dim_ffn % 128, dim % 256);
+ * Kernels (both GEMMs): bf16 runs on the matrix cores with block_m 32, 64,
+ * 128 or 256 when K is a multiple of 64 and the output columns a multiple of
+ * 8 (a partial last column tile clamps its weight rows and stores only the
+ * columns inside the matrix);
  * fp32 runs on the matrix cores (v_mfma_f32_16x16x4_f32) with block_m = 64,
  * K a multiple of 32 and dim_ffn % 32 == 0 (gate/up) or dim % 64 == 0 (down);
  * every other case on a general fp32-FMA kernel. Weights whose rows are a

@@ -146,6 +146,11 @@ GEMM_CASES = [
     # one 64-K step per tile, several tiles per workgroup: every step is a
     # tile's last and prefetches the next tile's first fragments
     (16384, 4, 2, 64, 1024, torch.bfloat16),
+    # partial last column tiles (dims multiples of 64, not of 128 / 256): 256-, 128- and 32-row tiles
+    (2048, 8, 2, 2880, 2880, torch.bfloat16),
+    (300, 16, 4, 192, 320, torch.bfloat16),
+    (64, 32, 4, 704, 576, torch.bfloat16),
+    (1024, 16, 4, 448, 960, torch.bfloat16),
     # fp32: matrix-core kernel (64-row tiles, K % 32 == 0) with each column-tile width, and the general kernel
     (1024, 8, 2, 512, 1024, torch.float32),  # gate/up 128-wide tiles, down 64-wide
     (4096, 16, 4, 1024, 512, torch.float32),  # 256-wide tiles for both
@@ -189,6 +194,7 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
     (64, 128, 8, 4096, 1536),  # decode-sized loads, some experts empty
     (16384, 4, 2, 256, 128),  # many rows per expert, several tiles per workgroup
     (1, 8, 2, 256, 128),  # one token
+    (2048, 8, 2, 2880, 2880),  # partial last column tile
 ])
 def test_gate_up_gather_bit_identical(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     # the gate/up GEMM reading x[sorted_token] directly equals the GEMM on the

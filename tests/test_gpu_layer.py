@@ -132,6 +132,23 @@ def test_shapes_and_shared_experts(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dt
     check_layer(layer, x, f"d{dim}_f{dim_ffn}_e{n_exp}_s{n_shared}_k{top_k}")
 
 
+@pytest.mark.parametrize("dim,dim_ffn,n_exp,n_shared,top_k,n_tok", [
+    (2880, 2880, 32, 1, 4, 2048),  # partial last column tiles in both GEMMs, 256-row tiles
+    (2880, 2880, 32, 0, 4, 64),  # the same at decode size (32-row tiles)
+    (704, 576, 16, 1, 4, 512),  # 128-row tiles
+    (192, 320, 8, 2, 2, 300),
+])
+def test_partial_column_tiles(gpu, dim, dim_ffn, n_exp, n_shared, top_k, n_tok):
+    # dims that are multiples of 64 but not of the column tiles (128 gate/up, 256 down): the bf16 matrix-core
+    # kernels clamp the last column tile's weight rows and store only the columns inside the matrix
+    assert ops.matrix_core_supported(dim, dim_ffn, torch.bfloat16)
+    assert dim_ffn % 128 or dim % 256
+    layer = _random_layer(gpu, dim, dim_ffn, n_exp, n_shared, top_k, torch.bfloat16)
+    g = torch.Generator(device=gpu).manual_seed(11)
+    x = torch.randn(1, n_tok, dim, generator=g, device=gpu).to(torch.bfloat16)
+    check_layer(layer, x, f"d{dim}_f{dim_ffn}_e{n_exp}_s{n_shared}_k{top_k}_t{n_tok}")
+
+
 def test_deterministic_repeat(gpu):
     layer, x = make_layer(WORKLOADS["moe_bf16_d2048_f1408_e64_k6_t8192"], gpu, n_tokens=1024)
     with torch.no_grad():

@@ -262,11 +262,15 @@ def test_block_m_policy():
 
 
 def test_packed_weights_follow_the_matrix_core_policy():
-    # the layer packs exactly the shapes the matrix-core kernels take
-    for dim, dim_ffn in [(4096, 14336), (2048, 1408), (256, 512), (512, 256), (96, 80), (8, 16), (256, 64)]:
+    # matrix-core shapes (dims multiples of 64) get the matrix-core tile heights; the layer packs those of
+    # them whose column tiles are whole (dim % 256, dim_ffn % 128)
+    for dim, dim_ffn in [(4096, 14336), (2048, 1408), (256, 512), (512, 256), (96, 80), (8, 16), (256, 64),
+                         (2880, 2880), (192, 320)]:
         for dtype in (torch.bfloat16, torch.float32):
             bm = ops.select_block_m(1024, 8, 2, dim, dim_ffn, dtype)  # 256 rows per expert: 256-row MFMA tiles
-            assert ops.packed_supported(dim, dim_ffn, dtype) == (bm == 256), (dim, dim_ffn, dtype)
+            assert ops.matrix_core_supported(dim, dim_ffn, dtype) == (bm == 256), (dim, dim_ffn, dtype)
+            whole = dim % 256 == 0 and dim_ffn % 128 == 0
+            assert ops.packed_supported(dim, dim_ffn, dtype) == (bm == 256 and whole), (dim, dim_ffn, dtype)
     m = DeepSeekMoE(512, 256, 4, n_shared_experts=0)
     assert not m.pack_weights and not m.uses_packed_weights(torch.bfloat16)  # opt-in
     m.pack_weights = True
