@@ -322,13 +322,14 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
 }
 
 // ---------------------------------------------------------------------------
-// Training forward and backward. bf16 with dim % 256 == 0 and dim_ffn % 128 ==
-// 0 runs the matrix-core kernels (256-row tile lists); every other shape and
-// fp32 runs the general-shape kernels (any tile height).
+// Training forward and backward. bf16 with dim and dim_ffn multiples of 64
+// runs the matrix-core kernels (256-row tile lists; partial last column tiles
+// clamp and mask); every other shape and fp32 runs the general-shape kernels
+// (any tile height).
 // ---------------------------------------------------------------------------
 
 static bool mfma_train_shape(int dtype, int64_t dim, int64_t dim_ffn) {
-  return dtype == ASTRAI_MOE_BF16 && dim > 0 && dim_ffn > 0 && dim % 256 == 0 && dim_ffn % 128 == 0 &&
+  return dtype == ASTRAI_MOE_BF16 && dim > 0 && dim_ffn > 0 && dim % 64 == 0 && dim_ffn % 64 == 0 &&
          dim <= (1ll << 22) && dim_ffn <= (1ll << 22);
 }
 

@@ -458,9 +458,9 @@ def moe_routed_forward(x: torch.Tensor, logits: torch.Tensor, w_gate: torch.Tens
 
 def backward_on_matrix_cores(dim: int, dim_ffn: int, dtype: torch.dtype) -> bool:
     """Whether training runs the matrix-core kernels for this expert shape
-    (bf16, dim % 256 == 0, dim_ffn % 128 == 0; 256-row tile lists). Every
-    other shape and fp32 runs the general-shape kernels."""
-    return packed_supported(dim, dim_ffn, dtype)
+    (bf16, dim and dim_ffn multiples of 64; 256-row tile lists). Every other
+    shape and fp32 runs the general-shape kernels."""
+    return matrix_core_supported(dim, dim_ffn, dtype)
 
 
 TRAIN_BLOCK_M = 256  # row-tile height of the matrix-core training kernels

@@ -5,8 +5,8 @@ The reference layer is plain torch, so autograd differentiates it op by op
 the HIP kernels with saving epilogues (the gate and up projections ``g, u``,
 ``h`` and the unweighted expert output ``y``), and the backward on grouped
 HIP kernels (``astrai_moe_row_grad``, ``astrai_moe_gemm_dgrad_*``,
-``astrai_moe_gemm_wgrad``): bf16 with dim % 256 == 0 and dim_ffn % 128 == 0 on
-the matrix cores, every other shape and fp32 on the general-shape kernels.
+``astrai_moe_gemm_wgrad``): bf16 with dim and dim_ffn multiples of 64 on the
+matrix cores, every other shape and fp32 on the general-shape kernels.
 They evaluate the formulas autograd applies to mlp.py:22-25 and :97-98 at
 autograd's rounding points (per expert e: ``dy = dout[tok] * w``,
 ``dw = sum(dout[tok] * y)``, ``dh = dy W_down``, ``du = dh silu(g)``,

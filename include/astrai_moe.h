@@ -302,8 +302,8 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
  * The reference gets its gradients from torch autograd over mlp.py:22-25
  * and :89-98; these entry points compute the same quantities with grouped
  * kernels, at autograd's rounding points (identities in fp32): on the matrix
- * cores for bf16 with dim % 256 == 0 and dim_ffn % 128 == 0 (tile lists built
- * with block_m = 256), on the general-shape kernels for every other shape and
+ * cores for bf16 with dim and dim_ffn multiples of 64 (tile lists built with
+ * block_m = 256), on the general-shape kernels for every other shape and
  * for fp32 (any block_m; the fp32 training forward takes the fp32 matrix-core
  * GEMMs where astrai_moe_gemm_gate_up / _down would). Per expert e with
  * permuted rows R_e:

@@ -143,7 +143,7 @@ def test_moe_backward(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, bias):
     _check_moe(layer, x, f"d{dim}_f{dim_ffn}_e{n_exp}_s{n_shared}_k{top_k}_{dtype}")
 
 
-@pytest.mark.parametrize("dim", [128, 256])  # general-shape / matrix-core backward kernels
+@pytest.mark.parametrize("dim", [120, 256])  # general-shape / matrix-core backward kernels
 def test_moe_backward_empty_experts(gpu, dim):
     # a sharp router leaves most of the 32 experts without tokens
     layer = _random_layer(gpu, dim, 256, 32, 0, 2, torch.bfloat16, router_scale=40.0, bias=True)
@@ -203,7 +203,7 @@ def test_moe_backward_zero_tokens(gpu, dim, dim_ffn, dtype, n_shared):
                 same(got, want, f"{group}{i}.{name}")
 
 
-@pytest.mark.parametrize("dim,dim_ffn", [(192, 320), (256, 384)])  # general-shape / matrix-core kernels
+@pytest.mark.parametrize("dim,dim_ffn", [(40, 24), (192, 320), (256, 384)])  # general-shape / matrix-core kernels
 def test_mlp_backward(gpu, dim, dim_ffn):
     torch.manual_seed(1)
     mlp = MLP(dim, dim_ffn).to(device=gpu, dtype=torch.bfloat16)
@@ -281,8 +281,8 @@ def _random_bwd_configs(n, seed):
     out = []
     for _ in range(n):
         if rnd.random() < 0.6:  # grouped backward kernels (bf16, matrix-core shapes)
-            dim, dim_ffn, dtype = 256 * rnd.randint(1, 3), 128 * rnd.randint(1, 5), torch.bfloat16
-        else:  # general-shape backward kernels
+            dim, dim_ffn, dtype = 64 * rnd.randint(1, 12), 64 * rnd.randint(1, 10), torch.bfloat16
+        else:  # general-shape backward kernels (also matrix-core ones where both dims are multiples of 64)
             dim, dim_ffn = 8 * rnd.randint(1, 24), 8 * rnd.randint(1, 24)
             dtype = rnd.choice([torch.bfloat16, torch.float32])
         n_exp = rnd.choice([1, 2, 4, 8, 16, 32])

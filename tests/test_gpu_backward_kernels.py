@@ -63,6 +63,8 @@ CASES = [
     (300, 16, 4, 512, 384, 0.0, BF),  # partial 256-column tiles, ~75 rows per expert
     (64, 128, 8, 256, 128, 0.0, BF),  # a few rows per expert, some experts empty
     (3000, 8, 2, 256, 640, 3.0, BF),  # skewed: one expert holds most rows
+    (1024, 8, 2, 704, 576, 0.0, BF),  # dims multiples of 64 only: partial last column tiles everywhere
+    (300, 8, 4, 192, 320, 1.0, BF),
     # general-shape kernels
     (300, 8, 2, 40, 24, 0.0, BF),  # the reference's tiny-config scale
     (200, 4, 2, 37, 30, 0.0, BF),  # dim_ffn % 4 == 2: a 2-column last block of g/u
