@@ -60,7 +60,8 @@ def register(name: str, sources: list[str] | None = None, **kwargs) -> None:
 register("moe_route")
 register("moe_permute")
 register("moe_gemm", sources=[str(KERNELS_DIR / "moe_gemm.hip"), str(KERNELS_DIR / "moe_gemm_mfma.hip"),
-                              str(KERNELS_DIR / "moe_gemm_mfma_f32.hip"), str(KERNELS_DIR / "moe_gemm_bwd.hip"),
+                              str(KERNELS_DIR / "moe_gemm_mfma_f32.hip"), str(KERNELS_DIR / "moe_gemm_mfma_f32_bwd.hip"),
+                              str(KERNELS_DIR / "moe_gemm_bwd.hip"),
                               str(KERNELS_DIR / "moe_gemm_generic_bwd.hip")])
 register("moe_combine")
 register("capi")

@@ -79,6 +79,25 @@ int launch_mfma_f32_down(const void* h, const int32_t* tiles, int64_t capacity,
                          int64_t dim, void* y, void* y_unweighted,
                          hipStream_t s);
 
+// fp32 backward on the matrix cores (moe_gemm_mfma_f32_bwd.hip): the dgrad
+// GEMMs over 64-row tile lists with K a multiple of 32 and N of 4, wgrad with
+// M and N multiples of 4; same contracts as the general-shape ones below.
+bool mfma_f32_bwd_supported(int64_t k, int64_t n, int block_m, const void* a,
+                            const void* c0, const void* c1, const void* e0);
+bool mfma_f32_wgrad_supported(int64_t m, int64_t n, const void* a,
+                              const void* b, const void* dw);
+int launch_mfma_f32_dgrad_down(const void* dy, const int32_t* tiles,
+                               int64_t capacity, const void* const* w_down,
+                               const void* gu, int64_t dim, int64_t dim_ffn,
+                               void* dg, void* du, hipStream_t s);
+int launch_mfma_f32_dgrad_in(const void* d, const int32_t* tiles,
+                             int64_t capacity, const void* const* w, int64_t k,
+                             int64_t n, const void* add, void* dx,
+                             hipStream_t s);
+int launch_mfma_f32_wgrad(const void* a, const void* b, const int32_t* offsets,
+                          int n_experts, int64_t m, int64_t n, void* dw,
+                          hipStream_t s);
+
 // Backward (moe_gemm_bwd.hip), bf16, 256-row tile lists:
 // dy = dout[sorted_token] * sorted_w and dw_rows = sum(dout[tok] * y) per row;
 int launch_row_grad(const void* dout, const int32_t* sorted_token,

@@ -429,6 +429,8 @@ extern "C" int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles, 
                    "gemm_dgrad_down: buffers must be 16-byte aligned");
     return launch_dgrad_down(dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, s);
   }
+  if (dtype == ASTRAI_MOE_F32 && mfma_f32_bwd_supported(dim, dim_ffn, block_m, dy, dg, du, gu))
+    return launch_mfma_f32_dgrad_down(dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, s);
   return launch_generic_dgrad_down(dtype, dy, tiles, capacity, w_down, gu, dim, dim_ffn, dg, du, s);
 }
 
@@ -452,6 +454,10 @@ extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, con
     if ((rc = launch_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
     return launch_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
   }
+  if (dtype == ASTRAI_MOE_F32 && mfma_f32_bwd_supported(dim_ffn, dim, block_m, dg, dx_perm, du, nullptr)) {
+    if ((rc = launch_mfma_f32_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
+    return launch_mfma_f32_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
+  }
   if ((rc = launch_generic_dgrad_in(dtype, dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
   return launch_generic_dgrad_in(dtype, du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
 }
@@ -471,5 +477,7 @@ extern "C" int astrai_moe_gemm_wgrad(const void* a, const void* b, const int32_t
   if (dtype == ASTRAI_MOE_BF16 && m % 8 == 0 && n % 8 == 0 && aligned16_ptr(a) && aligned16_ptr(b) &&
       aligned16_ptr(dw))
     return launch_wgrad(a, b, expert_offsets, n_experts, m, n, dw, s);
+  if (dtype == ASTRAI_MOE_F32 && mfma_f32_wgrad_supported(m, n, a, b, dw))
+    return launch_mfma_f32_wgrad(a, b, expert_offsets, n_experts, m, n, dw, s);
   return launch_generic_wgrad(dtype, a, b, expert_offsets, n_experts, m, n, dw, s);
 }

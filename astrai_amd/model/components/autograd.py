@@ -20,8 +20,9 @@ autograd's rounding points (per expert e: ``dy = dout[tok] * w``,
   their tokens in ascending expert order, rounding after every add, which is
   the combine kernel's contract (the reference's ``index_add_`` backward);
 * experts without rows get no gradient (the reference skips them, so their
-  ``.grad`` stays ``None`` there too) — one host synchronisation per backward,
-  after every kernel is enqueued.
+  ``.grad`` stays ``None`` there too): the forward copies the expert offsets
+  to pinned host memory behind its kernels, and the backward waits on that
+  copy's event, done long before, instead of on its own kernels.
 """
 
 from __future__ import annotations
@@ -70,6 +71,14 @@ class RoutedExperts(torch.autograd.Function):
         h, gu = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn)
         y, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_experts, dim)
         out = ops.moe_combine(y, perm.token_pos)
+        # which experts got rows, for the backward: copied to pinned host
+        # memory now, so that the backward reads it without waiting for its
+        # own kernels
+        offsets_host = torch.empty(n_experts + 1, dtype=torch.int32, pin_memory=True)
+        offsets_host.copy_(perm.expert_offsets, non_blocking=True)
+        ctx.offsets_ready = torch.cuda.Event()
+        ctx.offsets_ready.record()
+        ctx.offsets_host = offsets_host
         ctx.n_experts, ctx.block_m, ctx.tables = n_experts, bm, tables
         ctx.save_for_backward(perm.x_perm, perm.sorted_token, perm.sorted_w, perm.token_pos,
                               perm.expert_offsets, perm.tiles, h, gu, y_unw, *weights)
@@ -96,11 +105,12 @@ class RoutedExperts(torch.autograd.Function):
             d_gate = ops.moe_gemm_wgrad(dg, x_perm, offsets, n_experts)
             d_up = ops.moe_gemm_wgrad(du, x_perm, offsets, n_experts)
             d_down = ops.moe_gemm_wgrad(dy, h, offsets, n_experts)
-            # one host sync, after every kernel is enqueued: experts without
-            # rows get no gradient, as in the reference
-            counts = (offsets[1:] - offsets[:-1]).tolist()
-            for e, c in enumerate(counts):
-                if c > 0:
+            # experts without rows get no gradient, as in the reference; the
+            # offsets were copied to the host in the forward, long done by now
+            ctx.offsets_ready.synchronize()
+            offs = ctx.offsets_host.tolist()
+            for e in range(n_experts):
+                if offs[e + 1] > offs[e]:
                     g_gate[e], g_up[e], g_down[e] = d_gate[e], d_up[e], d_down[e]
         return (dx, dw, None, None, None, None, *g_gate, *g_up, *g_down)
 

@@ -303,10 +303,10 @@ int astrai_moe_combine(const void* y, const int32_t* token_pos,
  * and :89-98; these entry points compute the same quantities with grouped
  * kernels, at autograd's rounding points (identities in fp32): on the matrix
  * cores for bf16 with dim and dim_ffn multiples of 64 (tile lists built with
- * block_m = 256), on the general-shape kernels for every other shape and
- * for fp32 (any block_m; the fp32 training forward takes the fp32 matrix-core
- * GEMMs where astrai_moe_gemm_gate_up / _down would). Per expert e with
- * permuted rows R_e:
+ * block_m = 256); for fp32 on the fp32 matrix cores with block_m = 64 where
+ * the GEMM's K is a multiple of 32 and its output columns of 4 (the forward
+ * GEMMs as astrai_moe_gemm_gate_up / _down choose them); on the general-shape
+ * kernels for every other shape. Per expert e with permuted rows R_e:
  *
  *   forward   g = x W_gate^T, u = x W_up^T, h = u * silu(g), y = h W_down^T,
  *             out = sum over slots of y * w                    (mlp.py:22-24, :97-98)
