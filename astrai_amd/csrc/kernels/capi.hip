@@ -40,8 +40,8 @@ extern "C" const char* astrai_moe_last_error(void) { return g_last_error; }
 // Row-tile policy. The bf16 matrix-core kernels need K % 64 == 0 for both
 // GEMMs (dim and dim_ffn multiples of 64); other shapes and fp32 use 64-row
 // tiles (the fp32 matrix-core kernel's and the general kernel's). Among
-// matrix-core tiles (measured on MI355X, both GEMMs, one process, outputs
-// bit-identical across heights):
+// matrix-core tiles (measured on MI355X, both GEMMs, one process; the 32-,
+// 64- and 128-row tiles sum in the same order and give equal bits):
 // - routed experts, by average rows per expert: 32-row tiles below 24 rows
 //   (decode: the work is streaming the experts' weights), 64-row tiles below
 //   48, 128-row tiles below 128 (one tile per expert reads its weights once;
