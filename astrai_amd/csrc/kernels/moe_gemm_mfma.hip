@@ -618,18 +618,20 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_mfma_kernel(
   static_assert(!kPacked || Cfg::BN == 256, "packed weights come in 256-row tiles");
   TileSrc<Cfg::BM, Cfg::BN, kGateUp, kPacked, kGather> src;
   GatherRows<Cfg::A_PER_WAVE> grows;
-  // The K steps of column tile nt run from step (7 nt) mod KT around to the
-  // one before it, so the workgroups streaming at the same time read their
-  // weight rows at different K offsets. Starting every tile at step 0 puts
-  // the concurrent reads of rows that lie a power of two apart (8 KB rows at
-  // K = 4096, experts of one stacked allocation) at equal offsets, which
-  // measured 9 % slower on the decode gate/up GEMM. The start depends only
-  // on the column tile, so every tile height sums an output in the same order.
+  // The K steps of a tile of expert e run from step (7 e) mod KT around to
+  // the one before it, so the workgroups streaming different experts at the
+  // same time read their weight rows at different K offsets, while the
+  // column tiles of one expert still read its activation tile together (and
+  // share it in L2). Starting every tile at step 0 puts the concurrent reads
+  // of rows that lie a power of two apart (8 KB rows at K = 4096, experts of
+  // one stacked allocation) at equal offsets, which measured 11 % slower on
+  // the decode gate/up GEMM. The start depends only on the expert, so every
+  // tile height sums an output in the same order.
   const int kt_n = K / kBK;
   int k_start = 0;
   auto setup_tile = [&](int mt_, int nt_) {
     src.setup(tiles, A, W0, W1, K, N, mt_, nt_);
-    k_start = (nt_ * 7) % kt_n;
+    k_start = (tiles[ASTRAI_MOE_TILE_HEADER + (int64_t)mt_ * ASTRAI_MOE_TILE_STRIDE] * 7) % kt_n;
     if constexpr (kGather) grows.load(row_src, src.row0, src.rows, wave * Cfg::A_PER_WAVE, lane, k2);
   };
   auto issue_stage = [&](int kstep, int buf) {  // the tile's kstep-th step

@@ -52,8 +52,8 @@ MEASURED_TRAFFIC_BYTES: dict[str, float] = {
     "moe_bf16_d4096_f14336_e8_k2_t16384": (6155726.1 * 2 + 917505.3) * 1024,
     "moe_bf16_d2048_f1408_e64_k6_t8192": (779643.7 * 2 + 135168.2) * 1024,
     "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (760612.6 * 2 + 135168.1) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t64": (1577948.7 * 2 + 1540.6) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t1024": (1863876.0 * 2 + 24599.3) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t64": (1567671.9 * 2 + 1538.2) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t1024": (1681513.7 * 2 + 24587.2) * 1024,
     "moe_fp32_d512_f1024_e8_k2_t1024": (70495.9 * 2 + 8193.0) * 1024,
 }
 
