@@ -30,6 +30,29 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Wave-uniform (SGPR) copies of values every lane holds alike, such as tile
+// fields and weight pointers loaded at a tile boundary. Left in VGPRs, a value
+// loaded on the tile-boundary path but used by every step's DMA makes the
+// compiler wait for every load in flight (the LDS DMA of the stages ahead
+// included) before that use, once per step.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+template <typename T>
+__device__ __forceinline__ T* uniform(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<T*>(lo | (hi << 32));
+}
+
+// A load through the scalar cache (s_load), for data that nothing writes
+// while the kernel runs (tile lists, expert offsets, weight-pointer tables)
+// at a wave-uniform address. A vector load there would be counted by vmcnt
+// like the LDS DMA, and waiting for it would drain the stages in flight.
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)p;
+}
+
 __device__ inline void lds_dma_16(const void* gsrc, void* lds_dst) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)gsrc,
                                    (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);

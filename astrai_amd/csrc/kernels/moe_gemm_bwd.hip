@@ -106,10 +106,10 @@ struct RowTileWalk {
   __device__ int seek(int logical, TileInfo& t) const {
     logical = w.seek(logical, t.mt, t.nt);
     if (logical < total) {
-      const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)t.mt * ASTRAI_MOE_TILE_STRIDE;
-      t.e = ti[0];
-      t.row0 = ti[1];
-      t.rows = min(BwdCfg::BM, ti[2] - t.row0);
+      const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)uniform(t.mt) * ASTRAI_MOE_TILE_STRIDE;
+      t.e = load_scalar(ti);
+      t.row0 = load_scalar(ti + 1);
+      t.rows = min(BwdCfg::BM, load_scalar(ti + 2) - t.row0);
       t.ksteps = ksteps;
     }
     return logical;
@@ -136,8 +136,8 @@ struct ExpertWalk {
     const int in_group = r - first_m * NT;
     t.mt = first_m + in_group % gm;
     t.nt = in_group / gm;
-    t.row0 = off[t.e];
-    t.rows = off[t.e + 1] - t.row0;
+    t.row0 = load_scalar(off + t.e);
+    t.rows = load_scalar(off + t.e + 1) - t.row0;
     t.ksteps = (t.rows + kBK - 1) / kBK;
     return t.rows > 0;
   }
@@ -171,6 +171,37 @@ __device__ __forceinline__ void dma_mn(const char* base, int krow0, int valid_ro
   lds_dma_16(src, lds);
 }
 
+// A DMA wave's ops of one MN-major stage: groups q = dw * OPS + i. Lane
+// offset i of a tile, (2 i + lane / 32) * pitch + the lane's clamped column,
+// depends only on i (the swizzle z of K-row 2 q + lane / 32 does, OPS = 8),
+// so a step whose 64 K-rows all lie before valid_rows issues each op as a
+// uniform step base plus that 32-bit offset. Only an expert's last, partial
+// step takes the per-lane zero-row select.
+struct MnLanes {
+  uint32_t off[BwdCfg::OPS];
+  __device__ void setup(uint32_t pitch, uint32_t col0, uint32_t col_end, int lane) {
+#pragma unroll
+    for (int i = 0; i < BwdCfg::OPS; ++i)
+      off[i] = (uint32_t)(2 * i + (lane >> 5)) * pitch + min(col0 + mn_src_col(i, lane), col_end - 16u);
+  }
+};
+static_assert(BwdCfg::OPS == 8, "MN-major lane offsets repeat every 8 ops");
+
+__device__ __forceinline__ void dma_mn_step(const char* base, int krow0, int valid_rows, uint32_t pitch,
+                                            uint32_t col0, uint32_t col_end, const MnLanes& ml, int lane, int dw,
+                                            char* stage) {
+  constexpr int OPS = BwdCfg::OPS;
+  if (krow0 + kBK <= valid_rows) {
+    const char* sb = uniform(base + (int64_t)(krow0 + 2 * OPS * dw) * pitch);
+#pragma unroll
+    for (int i = 0; i < OPS; ++i) lds_dma_16(sb + ml.off[i], stage + (dw * OPS + i) * 1024);
+  } else {
+#pragma unroll
+    for (int i = 0; i < OPS; ++i)
+      dma_mn(base, krow0, valid_rows, pitch, col0, col_end, lane, dw * OPS + i, stage + (dw * OPS + i) * 1024);
+  }
+}
+
 // Per-tile global bases of both operands.
 template <Bwd kMode>
 struct BwdSrc {
@@ -178,37 +209,42 @@ struct BwdSrc {
   const char* b0 = nullptr;
   int rows = 0;
   uint32_t a_col0 = 0, b_col0 = 0;
-  __device__ void setup(const BwdArgs& p, const TileInfo& t) {
+  MnLanes a_mn, b_mn;  // a_mn: wgrad only
+  __device__ void setup(const BwdArgs& p, const TileInfo& t, int lane) {
     rows = t.rows;
     if constexpr (kMode == Bwd::kWgrad) {
-      a0 = reinterpret_cast<const char*>(p.a0 + (int64_t)t.row0 * p.M);
-      b0 = reinterpret_cast<const char*>(p.b_act + (int64_t)t.row0 * p.N);
+      a0 = uniform(reinterpret_cast<const char*>(p.a0 + (int64_t)t.row0 * p.M));
+      b0 = uniform(reinterpret_cast<const char*>(p.b_act + (int64_t)t.row0 * p.N));
       a_col0 = (uint32_t)t.mt * BwdCfg::MN_ROW;
       b_col0 = (uint32_t)t.nt * BwdCfg::MN_ROW;
+      a_mn.setup((uint32_t)p.M * 2u, a_col0, (uint32_t)p.M * 2u, lane);
     } else {
-      a0 = reinterpret_cast<const char*>(p.a0 + (int64_t)t.row0 * p.K);
-      b0 = static_cast<const char*>(p.w0[t.e]);
+      a0 = uniform(reinterpret_cast<const char*>(p.a0 + (int64_t)t.row0 * p.K));
+      b0 = static_cast<const char*>(load_scalar(p.w0 + t.e));
       b_col0 = (uint32_t)t.nt * BwdCfg::MN_ROW;
     }
+    b_mn.setup((uint32_t)p.N * 2u, b_col0, (uint32_t)p.N * 2u, lane);
   }
-  // 8-row group (dgrad, K-major) or 2-K-row group (wgrad, MN-major) q of
-  // step kstep's A stage.
-  __device__ void dma_a(const BwdArgs& p, int lane, int kstep, int q, char* lds) const {
+  // This DMA wave's share (groups dw * OPS ..) of step kstep's A stage: 8-row
+  // groups (dgrad, K-major) or 2-K-row groups (wgrad, MN-major).
+  __device__ void dma_a(const BwdArgs& p, int lane, int kstep, int dw, char* stage) const {
     if constexpr (kMode == Bwd::kWgrad) {
-      dma_mn(a0, kstep * kBK, rows, (uint32_t)p.M * 2u, a_col0, (uint32_t)p.M * 2u, lane, q, lds);
+      dma_mn_step(a0, kstep * kBK, rows, (uint32_t)p.M * 2u, a_col0, (uint32_t)p.M * 2u, a_mn, lane, dw, stage);
     } else {
       const DmaLane dl(lane, kstep);
-      const uint32_t row = (uint32_t)min(q * 8 + dl.row, rows - 1);
-      lds_dma_16(a0 + (row * ((uint32_t)p.K * 2u) + dl.chunk(q)), lds);
+#pragma unroll
+      for (int i = 0; i < BwdCfg::OPS; ++i) {
+        const int q = dw * BwdCfg::OPS + i;
+        const uint32_t row = (uint32_t)min(q * 8 + dl.row, rows - 1);
+        lds_dma_16(a0 + (row * ((uint32_t)p.K * 2u) + dl.chunk(q)), stage + q * 1024);
+      }
     }
   }
-  // 2-K-row group q of step kstep's B stage (MN-major in every mode).
-  __device__ void dma_b(const BwdArgs& p, int lane, int kstep, int q, char* lds) const {
-    if constexpr (kMode == Bwd::kWgrad) {
-      dma_mn(b0, kstep * kBK, rows, (uint32_t)p.N * 2u, b_col0, (uint32_t)p.N * 2u, lane, q, lds);
-    } else {
-      dma_mn(b0, kstep * kBK, 0x7fffffff, (uint32_t)p.N * 2u, b_col0, (uint32_t)p.N * 2u, lane, q, lds);
-    }
+  // This DMA wave's share of step kstep's B stage (MN-major in every mode;
+  // dgrad's weights have no rows to zero).
+  __device__ void dma_b(const BwdArgs& p, int lane, int kstep, int dw, char* stage) const {
+    const int valid = kMode == Bwd::kWgrad ? rows : 0x7fffffff;
+    dma_mn_step(b0, kstep * kBK, valid, (uint32_t)p.N * 2u, b_col0, (uint32_t)p.N * 2u, b_mn, lane, dw, stage);
   }
 };
 
@@ -218,16 +254,16 @@ struct BwdCursor {
   bool live;
   TileInfo t;
   BwdSrc<kMode> src;
-  __device__ void start(const BwdArgs& p, int logical_, const TileInfo& t_) {
+  __device__ void start(const BwdArgs& p, int logical_, const TileInfo& t_, int lane) {
     logical = logical_, t = t_, kt = 0, live = true;
-    src.setup(p, t);
+    src.setup(p, t, lane);
   }
-  __device__ void advance(const BwdArgs& p, const Walk& walk) {
+  __device__ void advance(const BwdArgs& p, const Walk& walk, int lane) {
     if (++kt == t.ksteps) {
       kt = 0;
       logical = walk.seek(logical + walk.G, t);
       live = logical < walk.total;
-      if (live) src.setup(p, t);
+      if (live) src.setup(p, t, lane);
     }
   }
 };
@@ -338,25 +374,15 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs
   if (wave >= Cfg::MW) {
     const int dw = wave - Cfg::MW;
     BwdCursor<kMode, Walk> ca, cb;
-    ca.start(p, logical, t);
-    cb.start(p, logical, t);
+    ca.start(p, logical, t, lane);
+    cb.start(p, logical, t, lane);
     auto issue_a = [&](int buf) {
-      char* base = smem + Cfg::A_OFF + buf * Cfg::A_BYTES;
-#pragma unroll
-      for (int i = 0; i < Cfg::OPS; ++i) {
-        const int q = dw * Cfg::OPS + i;
-        ca.src.dma_a(p, lane, ca.kt, q, base + q * 1024);
-      }
-      ca.advance(p, walk);
+      ca.src.dma_a(p, lane, ca.kt, dw, smem + Cfg::A_OFF + buf * Cfg::A_BYTES);
+      ca.advance(p, walk, lane);
     };
     auto issue_b = [&](int buf) {
-      char* base = smem + Cfg::B_OFF + buf * Cfg::B_BYTES;
-#pragma unroll
-      for (int i = 0; i < Cfg::OPS; ++i) {
-        const int q = dw * Cfg::OPS + i;
-        cb.src.dma_b(p, lane, cb.kt, q, base + q * 1024);
-      }
-      cb.advance(p, walk);
+      cb.src.dma_b(p, lane, cb.kt, dw, smem + Cfg::B_OFF + buf * Cfg::B_BYTES);
+      cb.advance(p, walk, lane);
     };
     int a_iss = 0, b_iss = 0;
     issue_b(0), ++b_iss;

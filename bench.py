@@ -316,16 +316,22 @@ def main():
         layer.requires_grad_(True)
         xg = x.detach().clone().requires_grad_(True)
         dout = torch.randn_like(x)
-        for _ in range(max(1, args.warmup // 2)):
-            layer(xg).backward(dout)
-        torch.cuda.synchronize()
-        b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        n_train = max(1, args.steps // 2)
-        b0.record()
-        for _ in range(n_train):
+
+        def train_step():
             layer.zero_grad(set_to_none=True)
             xg.grad = None
             layer(xg).backward(dout)
+
+        # the same loop body untimed first (allocator and host caches settle),
+        # then at least 10 timed steps: a short loop shows its start-up
+        for _ in range(max(2, args.warmup)):
+            train_step()
+        torch.cuda.synchronize()
+        b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n_train = max(10, args.steps)
+        b0.record()
+        for _ in range(n_train):
+            train_step()
         b1.record()
         torch.cuda.synchronize()
         train_ms = b0.elapsed_time(b1) / n_train
