@@ -353,6 +353,88 @@ __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][Bwd
   }
 }
 
+// dgrad_down's epilogue with its gu loads PF row blocks ahead of the stores.
+// The vector-memory counter retires loads and stores in issue order, so a
+// load issued after a row block's stores cannot be consumed before those
+// stores complete; here the accumulators are first rounded and transposed to
+// bf16 (half their registers), then each refill of the gu ring is issued
+// before the stores of the row block it follows. Same rounding points and
+// element order as bwd_epilogue.
+template <int PF>
+__device__ __forceinline__ void bwd_epilogue_swiglu(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16],
+                                                   const BwdArgs& p, const TileInfo& t, int wm, int wn) {
+  constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16, NJ = NT16 / 2;
+  static_assert(NT16 % 2 == 0 && PF <= MT16, "column pairs; ring depth");
+  const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int row_l = el & 15;
+  const int q = el >> 4;
+  const int nw = t.nt * BwdCfg::BN + wn * BwdCfg::WN;
+  bf16x8_t dh[MT16][NJ];  // lane: 8 consecutive columns of row block i, column pair j
+#pragma unroll
+  for (int i = 0; i < MT16; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      bf16x4_t e[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e[h][r] = (__bf16)acc[i][2 * j + h][r];
+      transpose2(e);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dh[i][j][r] = e[0][r], dh[i][j][4 + r] = e[1][r];
+    }
+  // element offset of the lane's 8 columns in row block i, column pair j (clamped
+  // inside the matrix for the loads; `ok`: the lane stores them)
+  auto offset = [&](int i, int j, bool& ok) -> int64_t {
+    const int gm = wm * BwdCfg::WM + i * 16 + row_l;
+    const int nn = nw + j * 32 + 8 * q;
+    ok = gm < t.rows && nn < p.N;
+    return (int64_t)(t.row0 + min(gm, t.rows - 1)) * p.N + min(nn, p.N - 8);
+  };
+  bf16x8_t g0[PF][NJ], g1[PF][NJ];
+  auto load = [&](int i, int slot) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      bool ok;
+      const int64_t off = offset(i, j, ok);
+      g0[slot][j] = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off);
+      g1[slot][j] = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off + 8);
+    }
+  };
+#pragma unroll
+  for (int b = 0; b < PF; ++b) load(b, b);
+#pragma unroll
+  for (int i = 0; i < MT16; ++i) {
+    const int slot = i % PF;
+    bf16x8_t o0[NJ], o1[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const bf16x8_t& gu = c < 4 ? g0[slot][j] : g1[slot][j];
+        const float d = (float)dh[i][j][c];
+        const float g = (float)gu[c & 3];
+        const float u = (float)gu[4 + (c & 3)];
+        const float s = sigmoid_f(g);
+        const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
+        o1[j][c] = (__bf16)(d * act);               // du
+        const float dact = (float)(__bf16)(d * u);
+        o0[j][c] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
+      }
+    }
+    if (i + PF < MT16) load(i + PF, slot);  // before this row block's stores
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      bool ok;
+      const int64_t off = offset(i, j, ok);
+      if (ok) {
+        *reinterpret_cast<bf16x8_t*>(p.c1 + off) = o1[j];
+        *reinterpret_cast<bf16x8_t*>(p.c0 + off) = o0[j];
+      }
+    }
+  }
+}
+
 template <Bwd kMode, typename Cfg = BwdCfg>
 __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs p) {
   using Walk = std::conditional_t<kMode == Bwd::kWgrad, ExpertWalk, RowTileWalk>;
@@ -496,7 +578,10 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs
       rotate();
     }
     __builtin_amdgcn_sched_barrier(0);
-    bwd_epilogue<kMode>(acc, p, t, wm, wn);
+    if constexpr (kMode == Bwd::kDgradDown)
+      bwd_epilogue_swiglu<2>(acc, p, t, wm, wn);
+    else
+      bwd_epilogue<kMode>(acc, p, t, wm, wn);
     logical = walk.seek(logical + walk.G, t);
     if (logical >= walk.total) break;
   }
