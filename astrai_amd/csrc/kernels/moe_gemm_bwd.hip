@@ -280,17 +280,16 @@ __device__ __forceinline__ float sigmoid_f(float g) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
 }
 
-// Epilogue from the accumulators (lane: row 16 i + l % 16, columns 16 j +
-// 4 (l / 16) .. + 3 of the wave's block). The accumulators are rounded to
-// bf16 and, per pair of 16-column tiles, go through the lane-group transpose,
-// which leaves each lane 8 consecutive columns of its row; the elementwise
-// inputs (gu, the added gradient) are then read for exactly those columns
-// (16 / 32 contiguous bytes) and the outputs stored as 16-byte pieces. N is
-// a multiple of 8, so a lane's 8 columns are wholly inside the matrix or
-// wholly past its edge.
+// Epilogue of the plain GEMMs (dgrad_in, wgrad) from the accumulators (lane:
+// row 16 i + l % 16, columns 16 j + 4 (l / 16) .. + 3 of the wave's block).
+// The accumulators are rounded to bf16 and, per pair of 16-column tiles, go
+// through the lane-group transpose, which leaves each lane 8 consecutive
+// columns of its row, stored as one 16-byte piece. N is a multiple of 8, so a
+// lane's 8 columns are wholly inside the matrix or wholly past its edge.
 template <Bwd kMode>
 __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16], const BwdArgs& p,
                                              const TileInfo& t, int wm, int wn) {
+  static_assert(kMode == Bwd::kDgradIn || kMode == Bwd::kWgrad, "no elementwise input");
   constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16;
   static_assert(NT16 % 2 == 0, "tiles are transposed in pairs");
   const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
@@ -322,48 +321,28 @@ __device__ __forceinline__ void bwd_epilogue(f32x4_t (&acc)[BwdCfg::WM / 16][Bwd
       if (!row_ok || nn >= p.N) continue;
       const int64_t off = row_off + nn;
       bf16x8_t o0;
-      if constexpr (kMode == Bwd::kDgradDown) {
-        // gu keeps g[c..c+3], u[c..c+3] at 2 c: the lane's 8 columns are 32 contiguous bytes
-        const bf16x8_t gu0 = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off);
-        const bf16x8_t gu1 = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off + 8);
-        bf16x8_t o1;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const bf16x8_t& gu = c < 4 ? gu0 : gu1;
-          const float dh = (float)e[c >> 2][c & 3];
-          const float g = (float)gu[c & 3];
-          const float u = (float)gu[4 + (c & 3)];
-          const float s = sigmoid_f(g);
-          const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
-          o1[c] = (__bf16)(dh * act);                 // du
-          const float dact = (float)(__bf16)(dh * u);
-          o0[c] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
-        }
-        *reinterpret_cast<bf16x8_t*>(p.c1 + off) = o1;
-      } else if constexpr (kMode == Bwd::kDgradInAdd) {
-        const bf16x8_t add = *reinterpret_cast<const bf16x8_t*>(p.e0 + off);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) o0[c] = (__bf16)((float)e[c >> 2][c & 3] + (float)add[c]);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) o0[c] = e[c >> 2][c & 3];
-      }
+      for (int c = 0; c < 8; ++c) o0[c] = e[c >> 2][c & 3];
       *reinterpret_cast<bf16x8_t*>(p.c0 + off) = o0;
     }
   }
 }
 
-// dgrad_down's epilogue with its gu loads PF row blocks ahead of the stores.
-// The vector-memory counter retires loads and stores in issue order, so a
-// load issued after a row block's stores cannot be consumed before those
-// stores complete; here the accumulators are first rounded and transposed to
-// bf16 (half their registers), then each refill of the gu ring is issued
-// before the stores of the row block it follows. Same rounding points and
-// element order as bwd_epilogue.
-template <int PF>
-__device__ __forceinline__ void bwd_epilogue_swiglu(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16],
-                                                   const BwdArgs& p, const TileInfo& t, int wm, int wn) {
+// The epilogues that read an elementwise input (dgrad_down: gu; dgrad_in_add:
+// the first projection's input gradient), with those loads PF row blocks
+// ahead of the stores. The vector-memory counter retires loads and stores in
+// issue order, so a load issued after a row block's stores cannot be consumed
+// before those stores complete; here the accumulators are first rounded and
+// transposed to bf16 (half their registers), then each refill of the input
+// ring is issued before the stores of the row block it follows. Same rounding
+// points and element order as bwd_epilogue.
+template <Bwd kMode, int PF>
+__device__ __forceinline__ void bwd_epilogue_pf(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16], const BwdArgs& p,
+                                                const TileInfo& t, int wm, int wn) {
+  static_assert(kMode == Bwd::kDgradDown || kMode == Bwd::kDgradInAdd, "epilogues with an elementwise input");
+  constexpr bool kSwiGlu = kMode == Bwd::kDgradDown;
   constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16, NJ = NT16 / 2;
+  constexpr int NL = kSwiGlu ? 2 : 1;  // 16-byte input loads per lane and column pair
   static_assert(NT16 % 2 == 0 && PF <= MT16, "column pairs; ring depth");
   const int el = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   const int row_l = el & 15;
@@ -391,14 +370,15 @@ __device__ __forceinline__ void bwd_epilogue_swiglu(f32x4_t (&acc)[BwdCfg::WM / 
     ok = gm < t.rows && nn < p.N;
     return (int64_t)(t.row0 + min(gm, t.rows - 1)) * p.N + min(nn, p.N - 8);
   };
-  bf16x8_t g0[PF][NJ], g1[PF][NJ];
+  bf16x8_t in[PF][NJ][NL];
   auto load = [&](int i, int slot) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       bool ok;
       const int64_t off = offset(i, j, ok);
-      g0[slot][j] = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off);
-      g1[slot][j] = *reinterpret_cast<const bf16x8_t*>(p.e0 + 2 * off + 8);
+#pragma unroll
+      for (int l = 0; l < NL; ++l)
+        in[slot][j][l] = *reinterpret_cast<const bf16x8_t*>(p.e0 + (kSwiGlu ? 2 * off + 8 * l : off));
     }
   };
 #pragma unroll
@@ -411,15 +391,20 @@ __device__ __forceinline__ void bwd_epilogue_swiglu(f32x4_t (&acc)[BwdCfg::WM / 
     for (int j = 0; j < NJ; ++j) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const bf16x8_t& gu = c < 4 ? g0[slot][j] : g1[slot][j];
         const float d = (float)dh[i][j][c];
-        const float g = (float)gu[c & 3];
-        const float u = (float)gu[4 + (c & 3)];
-        const float s = sigmoid_f(g);
-        const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
-        o1[j][c] = (__bf16)(d * act);               // du
-        const float dact = (float)(__bf16)(d * u);
-        o0[j][c] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
+        if constexpr (kSwiGlu) {
+          // gu keeps g[c..c+3], u[c..c+3] at 2 c: the lane's 8 columns are two 16-byte loads
+          const bf16x8_t& gu = in[slot][j][c >> 2];
+          const float g = (float)gu[c & 3];
+          const float u = (float)gu[4 + (c & 3)];
+          const float s = sigmoid_f(g);
+          const float act = (float)(__bf16)(g * s);  // silu(g) as the forward rounded it
+          o1[j][c] = (__bf16)(d * act);               // du
+          const float dact = (float)(__bf16)(d * u);
+          o0[j][c] = (__bf16)(dact * (s * (1.0f + g * (1.0f - s))));  // dg
+        } else {
+          o0[j][c] = (__bf16)(d + (float)in[slot][j][0][c]);
+        }
       }
     }
     if (i + PF < MT16) load(i + PF, slot);  // before this row block's stores
@@ -428,7 +413,7 @@ __device__ __forceinline__ void bwd_epilogue_swiglu(f32x4_t (&acc)[BwdCfg::WM / 
       bool ok;
       const int64_t off = offset(i, j, ok);
       if (ok) {
-        *reinterpret_cast<bf16x8_t*>(p.c1 + off) = o1[j];
+        if constexpr (kSwiGlu) *reinterpret_cast<bf16x8_t*>(p.c1 + off) = o1[j];
         *reinterpret_cast<bf16x8_t*>(p.c0 + off) = o0[j];
       }
     }
@@ -578,8 +563,12 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs
       rotate();
     }
     __builtin_amdgcn_sched_barrier(0);
+    // input rings two (gu, 32 bytes per lane and column pair) and four row
+    // blocks deep: deeper rings spilled
     if constexpr (kMode == Bwd::kDgradDown)
-      bwd_epilogue_swiglu<2>(acc, p, t, wm, wn);
+      bwd_epilogue_pf<kMode, 2>(acc, p, t, wm, wn);
+    else if constexpr (kMode == Bwd::kDgradInAdd)
+      bwd_epilogue_pf<kMode, 4>(acc, p, t, wm, wn);
     else
       bwd_epilogue<kMode>(acc, p, t, wm, wn);
     logical = walk.seek(logical + walk.G, t);
