@@ -29,6 +29,10 @@ kernels and so does the backward (grouped dgrad / wgrad kernels,
 
 from __future__ import annotations
 
+from functools import partial
+from itertools import chain
+from operator import attrgetter, is_not, itemgetter, methodcaller
+
 import torch
 import torch.nn as nn
 from torch import Tensor
@@ -102,6 +106,27 @@ class MLP(nn.Module):
         return out.view(*lead, dim)
 
 
+_modules_of = attrgetter("_modules")
+_params_of = attrgetter("_parameters")
+_weight_of = itemgetter("weight")
+_bias_of = methodcaller("get", "bias")
+_is_set = partial(is_not, None)
+_requires_grad = attrgetter("requires_grad")
+
+
+class _ExpertState:
+    """A DeepSeekMoE's validated expert weights (routed and shared, each as
+    gate, up, down lists), their dtype and device, and the device pointer
+    tables built from them; ``sig`` identifies the modules, parameter objects
+    and storages they were read from."""
+
+    __slots__ = ("sig", "ptrs", "routed", "shared", "flat", "dtype", "device", "tables")
+
+    def __init__(self, sig, ptrs, routed, shared, flat, dtype, device, tables):
+        self.sig, self.ptrs, self.routed, self.shared, self.flat = sig, ptrs, routed, shared, flat
+        self.dtype, self.device, self.tables = dtype, device, tables
+
+
 @FFNFactory.register("moe")
 class DeepSeekMoE(nn.Module):
     def __init__(
@@ -130,10 +155,9 @@ class DeepSeekMoE(nn.Module):
         self.routed_experts = nn.ModuleList(
             [MLP(dim, dim_ffn, down_init_std=down_init_std) for _ in range(n_routed_experts)]
         )
-        # Device pointer tables of the expert weights, rebuilt when any
-        # weight's storage moves (not part of the state_dict).
-        self._table_key: tuple | None = None
-        self._tables: tuple[Tensor, ...] | None = None
+        # The experts' validated weights and their device pointer tables
+        # (_current; not part of the state_dict).
+        self._state: _ExpertState | None = None
         # Opt-in, inference only: keep a packed copy of the routed experts'
         # weights in the order the GEMMs stage it (ops.moe_pack_*), rebuilt
         # when a weight moves or changes (its version counter), for bf16 shapes
@@ -143,7 +167,7 @@ class DeepSeekMoE(nn.Module):
         self.pack_weights = False
         self._packed: tuple | None = None
 
-    # -- weight-pointer tables -------------------------------------------------
+    # -- weights and their pointer tables ----------------------------------------
     def _expert_weights(self, experts: nn.ModuleList) -> tuple[list[Tensor], list[Tensor], list[Tensor]]:
         g, u, d = [], [], []
         for e in experts:
@@ -153,11 +177,45 @@ class DeepSeekMoE(nn.Module):
             d.append(wd)
         return g, u, d
 
-    def _weight_tables(self) -> tuple[Tensor, ...]:
-        routed = self._expert_weights(self.routed_experts)
+    def _current(self, dtype: torch.dtype, device: torch.device) -> _ExpertState:
+        """The experts' current weights and their device pointer tables.
+
+        Reading every expert weight through ``nn.Module`` attribute lookup
+        costs a few µs per expert on the host (at 128 experts ~0.6 ms per
+        forward, as much as the decode step's kernels). Here the modules'
+        registries (``_modules``, ``_parameters``) are read with C-level
+        ``map`` calls, and the full validation (bias-free ``Linear``
+        projections, one dtype and device) runs again only when a module, a
+        parameter object or a weight's storage differs from the last call. The
+        pointer tables are rebuilt only when a storage moved, so graphs
+        captured earlier keep valid tables. Every weight must be on ``device``
+        in ``dtype`` (the input's)."""
+        sig = None
+        try:
+            lins = []
+            for experts in (self.routed_experts, self.shared_experts):
+                children = list(map(_modules_of, experts._modules.values()))
+                lins += [list(map(itemgetter(n), children)) for n in ("gate", "up", "down")]
+            flat = list(chain.from_iterable(lins))
+            pdicts = list(map(_params_of, flat))
+            weights = list(map(_weight_of, pdicts))
+            if not any(map(_is_set, map(_bias_of, pdicts))):
+                sig = (tuple(map(id, flat)), tuple(map(id, weights)), tuple(map(Tensor.data_ptr, weights)))
+        except (KeyError, AttributeError, TypeError):
+            sig = None
+        st = self._state
+        if st is not None and sig is not None and sig == st.sig and st.dtype == dtype and st.device == device:
+            return st
+        routed = self._expert_weights(self.routed_experts)  # raises on non-Linear or biased projections
         shared = self._expert_weights(self.shared_experts)
-        key = tuple(w.data_ptr() for ws in (*routed, *shared) for w in ws)
-        if key != self._table_key or self._tables is None:
+        flat_w = [w for ws in (*routed, *shared) for w in ws]
+        for w in flat_w:
+            if w.device != device or w.dtype != dtype:
+                raise RuntimeError(f"DeepSeekMoE: parameters must be on {device} in {dtype}, found {w.device}/{w.dtype}")
+        ptrs = tuple(w.data_ptr() for w in flat_w)
+        if st is not None and st.ptrs == ptrs:
+            tables = st.tables
+        else:
             shape_in = tuple(routed[0][0].shape)
             shape_out = tuple(routed[2][0].shape)
             t_routed = (
@@ -169,11 +227,17 @@ class DeepSeekMoE(nn.Module):
                 tuple(ops.expert_weight_table([w], tuple(w.shape)) for w in (shared[0][i], shared[1][i], shared[2][i]))
                 for i in range(len(shared[0]))
             )
-            self._tables = (t_routed, t_shared)
-            self._table_key = key
-        return self._tables
+            tables = (t_routed, t_shared)
+        self._state = _ExpertState(sig, ptrs, routed, shared, flat_w, dtype, device, tables)
+        return self._state
 
-    def _packed_tables(self, dtype: torch.dtype) -> tuple[Tensor, Tensor] | None:
+    def _weight_tables(self) -> tuple[Tensor, ...]:
+        """(routed gate, up, down tables), per shared expert (gate, up, down),
+        for the weights' own dtype and device."""
+        w = self.routed_experts[0].gate.weight
+        return self._current(w.dtype, w.device).tables
+
+    def _packed_tables(self, dtype: torch.dtype, st: _ExpertState) -> tuple[Tensor, Tensor] | None:
         """Pointer tables of the packed gate/up and down copies, or None when
         this forward reads the live weights. The copies are rebuilt whenever a
         routed weight's storage or version counter changes; the cache holds a
@@ -181,7 +245,7 @@ class DeepSeekMoE(nn.Module):
         reused by another tensor while the copy made from it is in use."""
         if not self.uses_packed_weights(dtype):
             return None
-        g, u, d = self._expert_weights(self.routed_experts)
+        g, u, d = st.routed
         srcs = [w for ws in (g, u, d) for w in ws]
         if any(w.is_inference() for w in srcs):  # no version counter to follow
             return None
@@ -207,22 +271,24 @@ class DeepSeekMoE(nn.Module):
         # the reference's view (mlp.py:66), then a dense copy when the view is
         # strided (e.g. a slice of a wider buffer): the kernels take dense rows
         x_flat = x.view(-1, dim).contiguous()
-        params = list(self.parameters())
-        _check_gpu_input(x_flat, params, "DeepSeekMoE")
-        if _needs_grad(x_flat, params):
-            return self._forward_autograd(x_flat).view(bsz, seq_len, dim)
-        shared_out = self._shared_forward(x_flat)
-        out = self._routed_forward(x_flat, shared_out)
+        router_w = self.router.weight
+        _check_gpu_input(x_flat, [router_w], "DeepSeekMoE")
+        st = self._current(x_flat.dtype, x_flat.device)
+        if torch.is_grad_enabled() and (x_flat.requires_grad or router_w.requires_grad
+                                        or any(map(_requires_grad, st.flat))):
+            return self._forward_autograd(x_flat, st).view(bsz, seq_len, dim)
+        shared_out = self._shared_forward(x_flat, st)
+        out = self._routed_forward(x_flat, st, shared_out)
         return out.view(bsz, seq_len, dim)
 
-    def _shared_forward(self, x: Tensor) -> Tensor | None:
+    def _shared_forward(self, x: Tensor, st: _ExpertState) -> Tensor | None:
         """Each shared expert's output stacked as ``[n_shared, T, D]``; the
         mean (``mlp.py:77``) is taken inside the combine kernel. ``None`` for
         ``n_shared_experts == 0`` (the reference's ``zeros_like``)."""
         if self.n_shared_experts == 0 or x.shape[0] == 0:
             return None
-        _, t_shared = self._weight_tables()
-        dim_ffn = self.shared_experts[0].up.weight.shape[0]
+        _, t_shared = st.tables
+        dim_ffn = st.shared[1][0].shape[0]
         out = torch.empty(self.n_shared_experts, x.shape[0], x.shape[1], dtype=x.dtype, device=x.device)
         # one tile list for every shared expert: they run over the same rows
         tiles = ops.dense_tiles(x.shape[0], ops.dense_block_m(x.shape[0], x.shape[1], dim_ffn, x.dtype), x.device)
@@ -230,20 +296,20 @@ class DeepSeekMoE(nn.Module):
             ops.moe_dense_mlp(x, tg, tu, td, dim_ffn, out=out[i], tiles=tiles)
         return out
 
-    def _routed_forward(self, x: Tensor, shared: Tensor | None = None) -> Tensor:
-        dim_ffn = self.routed_experts[0].up.weight.shape[0]
-        packed_tables = self._packed_tables(x.dtype)
+    def _routed_forward(self, x: Tensor, st: _ExpertState, shared: Tensor | None = None) -> Tensor:
+        dim_ffn = st.routed[1][0].shape[0]
+        packed_tables = self._packed_tables(x.dtype, st)
         packed = packed_tables is not None
         if packed:
             tg, td = packed_tables
             tu = tg
         else:
-            (tg, tu, td), _ = self._weight_tables()
+            tg, tu, td = st.tables[0]
         logits = self.router(x)
         return ops.moe_routed_forward(x, logits, tg, tu, td, dim_ffn, self.n_activated_experts, shared,
                                       packed=packed)
 
-    def _forward_autograd(self, x: Tensor) -> Tensor:
+    def _forward_autograd(self, x: Tensor, st: _ExpertState) -> Tensor:
         """mlp.py:64-100 with autograd: HIP kernels forward and backward.
         Routing indices come from the route kernel; the weights are rebuilt
         from the logits with torch ops (same values) so their gradient reaches
@@ -254,9 +320,9 @@ class DeepSeekMoE(nn.Module):
             # shared experts connect the output to x and to parameters
             if self.n_shared_experts == 0:
                 return x.new_zeros(0, x.shape[1])
-            return EmptyBatch.apply(x, *[w for ws in self._expert_weights(self.shared_experts) for w in ws])
-        t_routed, t_shared = self._weight_tables()
-        routed_w = self._expert_weights(self.routed_experts)
+            return EmptyBatch.apply(x, *[w for ws in st.shared for w in ws])
+        t_routed, t_shared = st.tables
+        routed_w = st.routed
         dim_ffn = routed_w[0][0].shape[0]
         logits = self.router(x)
         route = ops.moe_route(logits.detach(), self.n_activated_experts)
@@ -265,7 +331,7 @@ class DeepSeekMoE(nn.Module):
                                      *routed_w[0], *routed_w[1], *routed_w[2])
         if self.n_shared_experts == 0:
             return routed
-        shared_w = self._expert_weights(self.shared_experts)
+        shared_w = st.shared
         shared = sum(
             DenseExpert.apply(x, t_shared[i], dim_ffn, shared_w[0][i], shared_w[1][i], shared_w[2][i])
             for i in range(self.n_shared_experts)
