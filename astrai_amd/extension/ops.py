@@ -64,7 +64,15 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed ({rc}): {loader.last_error()}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    """The current stream of t's device as a raw handle (the same value as
+    ``torch.cuda.current_stream(t.device).cuda_stream``, without building the
+    Python stream object: ~5 µs of host time per call)."""
+    if _raw_stream is not None and t.device.type == "cuda":
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -122,3 +122,14 @@ def test_graph_survives_many_eager_token_counts(gpu):
             torch.cuda.synchronize()
             assert torch.equal(static_out, eager), f"replay {i} after the eager calls differs"
         _assert_oracle(layer, static_x, static_out, "replay after 70 eager token counts")
+
+
+def test_launch_stream_is_the_current_stream(gpu):
+    # every launch goes to the caller's current stream: the raw handle the
+    # wrappers pass equals torch's, on the default stream and on a side stream
+    t = torch.zeros(4, device=gpu)
+    assert ops._stream(t) == torch.cuda.current_stream(gpu).cuda_stream
+    side = torch.cuda.Stream(device=gpu)
+    with torch.cuda.stream(side):
+        assert ops._stream(t) == side.cuda_stream != torch.cuda.default_stream(gpu).cuda_stream
+    assert ops._stream(t) == torch.cuda.current_stream(gpu).cuda_stream
