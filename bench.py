@@ -317,8 +317,14 @@ def main():
         xg = x.detach().clone().requires_grad_(True)
         dout = torch.randn_like(x)
 
+        params = [p for p in layer.parameters() if p.requires_grad]
+
         def train_step():
-            layer.zero_grad(set_to_none=True)
+            # gradients cleared from a flat parameter list, as an optimizer's
+            # zero_grad(set_to_none=True) does (Module.zero_grad walks the
+            # module tree: ~0.8 ms of host time per step at 64 experts)
+            for p in params:
+                p.grad = None
             xg.grad = None
             layer(xg).backward(dout)
 
