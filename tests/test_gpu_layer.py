@@ -181,6 +181,48 @@ def test_checkpoint_load_into_live_layer(gpu, tmp_path):
 
 
 
+
+def test_live_layer_changes_are_seen(gpu):
+    # after a forward, every way of changing the experts must reach the next
+    # forward: a .data swap, a replaced expert, a requires_grad toggle; a
+    # projection replaced by another module type or given a bias must raise
+    from astrai_amd.model.components.linear import Linear
+    from astrai_amd.model.components.mlp import MLP
+
+    a = _random_layer(gpu, 128, 256, 8, 1, 2, torch.bfloat16, seed=0)
+    c = _random_layer(gpu, 128, 256, 8, 1, 2, torch.bfloat16, seed=3)
+    x = torch.randn(1, 96, 128, device=gpu).to(torch.bfloat16)
+    with torch.no_grad():
+        before = a(x)
+        a.routed_experts[1].up.weight.data = c.routed_experts[1].up.weight.data.clone()
+        assert not torch.equal(a(x), before)
+        check_layer(a, x, "data swap")
+        a.routed_experts[5] = c.routed_experts[5]
+        check_layer(a, x, "replaced expert")
+        a.shared_experts[0] = c.shared_experts[0]
+        check_layer(a, x, "replaced shared expert")
+    # a weight that starts requiring grad sends the next forward through autograd
+    a.routed_experts[2].down.weight.requires_grad_(True)
+    out = a(x)
+    assert out.grad_fn is not None
+    out.float().sum().backward()
+    assert a.routed_experts[2].down.weight.grad is not None
+    a.routed_experts[2].down.weight.requires_grad_(False)
+    with torch.no_grad():
+        check_layer(a, x, "grad toggled off")
+        keep = a.routed_experts[3].gate
+        a.routed_experts[3].gate = torch.nn.Sequential(keep)
+        with pytest.raises(RuntimeError, match="bias-free Linear"):
+            a(x)
+        a.routed_experts[3].gate = keep
+        check_layer(a, x, "projection restored")
+        keep.bias = torch.nn.Parameter(torch.zeros(256, device=gpu, dtype=torch.bfloat16))
+        with pytest.raises(RuntimeError, match="bias-free Linear"):
+            a(x)
+        keep.bias = None
+        check_layer(a, x, "bias removed")
+        assert isinstance(keep, Linear) and isinstance(a.routed_experts[3], MLP)
+
 def test_packed_weights_match_live_weights_and_follow_updates(gpu, tmp_path):
     # bf16 shapes the matrix-core kernels take are read from the layer's packed
     # copy in inference; its results must equal the live-weight path bit for
