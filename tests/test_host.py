@@ -390,3 +390,52 @@ def test_dense_tile_lists_are_not_cached_across_calls():
     # that later calls could clear and the allocator reuse
     assert not any("cache" in name for name in vars(ops) if name.startswith("_dense"))
     assert "astrai_moe_dense_tiles" in loader._SIGNATURES
+
+
+def test_use_hip_ffn_swaps_the_registry_entries():
+    # a registry with the reference factory's API (astrai/factory.py:45-147,
+    # restated by astrai_amd.factory): register() refuses taken names, so the
+    # switch writes the entries; models built afterwards get the HIP classes
+    # with the reference's kwarg filtering; restore_ffn puts the old ones back
+    import torch.nn as nn
+
+    from astrai_amd.factory import BaseFactory
+    from astrai_amd.integration import restore_ffn, use_hip_ffn
+    from astrai_amd.model.components.mlp import MLP, DeepSeekMoE
+
+    class FFN(BaseFactory[nn.Module]):
+        pass
+
+    @FFN.register("moe")
+    class TorchMoE(nn.Module):
+        def __init__(self, dim, dim_ffn, n_routed_experts, n_shared_experts=1, n_activated_experts=2):
+            super().__init__()
+
+    @FFN.register("mlp")
+    class TorchMLP(nn.Module):
+        def __init__(self, dim, dim_ffn):
+            super().__init__()
+
+    with pytest.raises(ValueError):
+        FFN.register("moe")(DeepSeekMoE)  # why the switch writes the registry
+    prev = use_hip_ffn(FFN)
+    assert FFN._entries["moe"] is DeepSeekMoE and FFN._entries["mlp"] is TorchMLP
+    cfg = dict(dim=64, dim_ffn=128, n_routed_experts=4, n_shared_experts=1, n_activated_experts=2, n_layers=2,
+               n_heads=8, n_kv_heads=2, norm_eps=1e-5, down_init_std=0.01)  # a decoder block's whole cfg
+    m = FFN.create("moe", **cfg)
+    assert isinstance(m, DeepSeekMoE) and m.n_routed_experts == 4 and len(m.shared_experts) == 1
+    assert "routed_experts.3.down.weight" in m.state_dict() and "router.weight" in m.state_dict()
+    restore_ffn(prev, FFN)
+    assert FFN._entries["moe"] is TorchMoE and FFN._entries["mlp"] is TorchMLP
+    prev = use_hip_ffn(FFN, moe=False, mlp=True)
+    assert FFN._entries["mlp"] is MLP and FFN._entries["moe"] is TorchMoE
+    assert isinstance(FFN.create("mlp", **cfg), MLP)
+    restore_ffn(prev, FFN)
+    assert FFN._entries["mlp"] is TorchMLP
+
+    class Other(BaseFactory[dict]):  # the classes must satisfy the registry's base type
+        pass
+
+    with pytest.raises(TypeError):
+        use_hip_ffn(Other)
+    assert "moe" not in Other._entries
