@@ -96,8 +96,9 @@ struct TileWalk {
   // are exactly [0, total) and each round but the last is full. (Sizing the
   // last group by the list's capacity instead spread its live tiles over
   // several mostly empty rounds.)
-  __device__ TileWalk(const int32_t* tiles, int capacity, int n_tiles_n)
-      : G((int)gridDim.x),
+  // G: the workgroups walking the list (the launch's grid unless given)
+  __device__ TileWalk(const int32_t* tiles, int capacity, int n_tiles_n, int G_ = 0)
+      : G(G_ > 0 ? G_ : (int)gridDim.x),
         n_live(min(tiles[0], min(tiles[2], capacity))),
         total(n_live * n_tiles_n),
         group_size(GM * n_tiles_n) {}

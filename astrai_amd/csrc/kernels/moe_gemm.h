@@ -20,6 +20,15 @@ constexpr int kMfmaMidBM = 64;
 // its weights once where two 64-row tiles would stream them twice.
 constexpr int kMfmaMid2BM = 128;
 
+// Partial-sum buffer of the 256-row kernels' split tail (fp32; none: the last
+// round's tiles run whole). split_buffer_bytes() lets every launch on the
+// current device split: one 256 x 256 fp32 tile per compute unit.
+struct SplitBuffer {
+  float* part = nullptr;
+  int64_t bytes = 0;
+};
+int64_t split_buffer_bytes();
+
 // Shape constraints of the bf16 kernels: K a multiple of 64, the output
 // columns a multiple of the column tile, 16-byte aligned operands.
 bool mfma_gate_up_supported(int64_t dim, int64_t dim_ffn, int block_m,
@@ -36,7 +45,8 @@ int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles,
 int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
                      const void* const* w_down, const void* sorted_w,
                      int64_t dim_ffn, int64_t dim, int block_m, bool packed,
-                     void* y, hipStream_t s);
+                     void* y, hipStream_t s,
+                     const SplitBuffer& split = {});
 
 // As launch_mfma_gate_up, reading the activation rows as x[sorted_token[r]]
 // (x: [n_tokens, dim]) instead of a copied x_perm.
@@ -59,7 +69,8 @@ int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles,
 int launch_mfma_down_save(const void* h, const int32_t* tiles,
                           int64_t capacity, const void* const* w_down,
                           const void* sorted_w, int64_t dim_ffn, int64_t dim,
-                          void* y, void* y_unweighted, hipStream_t s);
+                          void* y, void* y_unweighted, hipStream_t s,
+                          const SplitBuffer& split = {});
 
 // fp32 on the matrix cores (moe_gemm_mfma_f32.hip), 64-row tile lists, K a
 // multiple of 32, output columns a multiple of 32 (gate/up) or 64 (down),

@@ -169,6 +169,16 @@ int check_common(const char* who, const void* A, const int32_t* tiles,
   return ASTRAI_MOE_OK;
 }
 
+// The split-tail workspace: optional; when given, 16-byte aligned with a
+// non-negative size (a size below astrai_moe_gemm_split_bytes() leaves the
+// tail whole).
+int check_split(const char* who, const void* workspace, int64_t workspace_bytes) {
+  ASTRAI_REQUIRE(workspace_bytes >= 0, "%s: negative workspace size %lld", who, (long long)workspace_bytes);
+  ASTRAI_REQUIRE(workspace == nullptr || reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+                 "%s: workspace must be 16-byte aligned", who);
+  return ASTRAI_MOE_OK;
+}
+
 }  // namespace
 }  // namespace astrai_moe
 
@@ -231,11 +241,13 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                                     const void* sorted_w, int dtype,
                                     int64_t n_rows, int n_experts,
                                     int64_t dim_ffn, int64_t dim, int block_m,
-                                    void* y, void* stream) {
+                                    void* y, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
   clear_error();
   int rc = check_common("gemm_down", h, tiles, tiles_len, dtype, n_rows,
                         n_experts, dim_ffn, dim, block_m, y);
   if (rc) return rc;
+  if ((rc = check_split("gemm_down", workspace, workspace_bytes))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_down, "gemm_down: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
@@ -243,7 +255,8 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
   if (dtype == ASTRAI_MOE_BF16) {
     if (mfma_down_supported(dim_ffn, dim, block_m, h, y))
       return launch_mfma_down(h, tiles, capacity, w_down, sorted_w, dim_ffn,
-                              dim, block_m, false, y, s);
+                              dim, block_m, false, y, s,
+                              SplitBuffer{static_cast<float*>(workspace), workspace_bytes});
     return launch_generic<bf16_t, false>(h, tiles, capacity, w_down, nullptr,
                                          sorted_w, dim_ffn, dim, y, s);
   }
@@ -253,6 +266,8 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
   return launch_generic<float, false>(h, tiles, capacity, w_down, nullptr,
                                       sorted_w, dim_ffn, dim, y, s);
 }
+
+extern "C" int64_t astrai_moe_gemm_split_bytes(void) { return split_buffer_bytes(); }
 
 static bool aligned16_ptr(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
@@ -305,11 +320,13 @@ extern "C" int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t*
 extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, int64_t tiles_len,
                                            const void* const* w_packed, const void* sorted_w, int dtype,
                                            int64_t n_rows, int n_experts, int64_t dim_ffn, int64_t dim,
-                                           int block_m, void* y, void* stream) {
+                                           int block_m, void* y, void* workspace, int64_t workspace_bytes,
+                                           void* stream) {
   clear_error();
   int rc = check_common("gemm_down_packed", h, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m,
                         y);
   if (rc) return rc;
+  if ((rc = check_split("gemm_down_packed", workspace, workspace_bytes))) return rc;
   ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_down_packed: packed weights are bf16 only");
   ASTRAI_REQUIRE(n_rows == 0 || (dim % 256 == 0 && mfma_down_supported(dim_ffn, dim, block_m, h, y)),
                  "gemm_down_packed: unsupported shape (dim_ffn %lld, dim %lld, block_m %d) or alignment",
@@ -318,7 +335,8 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
   ASTRAI_REQUIRE(w_packed, "gemm_down_packed: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   return launch_mfma_down(h, tiles, capacity, w_packed, sorted_w, dim_ffn, dim, block_m, true, y,
-                          static_cast<hipStream_t>(stream));
+                          static_cast<hipStream_t>(stream),
+                          SplitBuffer{static_cast<float*>(workspace), workspace_bytes});
 }
 
 // ---------------------------------------------------------------------------
@@ -371,10 +389,12 @@ extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* 
 extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, int64_t tiles_len,
                                           const void* const* w_down, const void* sorted_w, int dtype,
                                           int64_t n_rows, int n_experts, int64_t dim_ffn, int64_t dim, int block_m,
-                                          void* y, void* y_unweighted, void* stream) {
+                                          void* y, void* y_unweighted, void* workspace, int64_t workspace_bytes,
+                                          void* stream) {
   clear_error();
   int rc = check_common("gemm_down_train", h, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m, y);
   if (rc) return rc;
+  if ((rc = check_split("gemm_down_train", workspace, workspace_bytes))) return rc;
   if ((rc = check_train("gemm_down_train", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_down && sorted_w && y_unweighted, "gemm_down_train: null weight table, row weights or output");
@@ -383,7 +403,8 @@ extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, i
   if (mfma_train_shape(dtype, dim, dim_ffn)) {
     ASTRAI_REQUIRE(aligned16_ptr(h) && aligned16_ptr(y) && aligned16_ptr(y_unweighted),
                    "gemm_down_train: buffers must be 16-byte aligned");
-    return launch_mfma_down_save(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, y, y_unweighted, s);
+    return launch_mfma_down_save(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, y, y_unweighted, s,
+                                 SplitBuffer{static_cast<float*>(workspace), workspace_bytes});
   }
   if (dtype == ASTRAI_MOE_BF16)
     return launch_generic<bf16_t, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,

@@ -350,29 +350,85 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
   }
 }
 
-// Position of a DMA wave in this workgroup's step sequence: the tile and K
-// step it loads next, and that tile's global bases.
-template <int BM, int BN, int GM, bool kGateUp, bool kPacked, bool kGather = false>
-struct StepCursor {
-  int logical, mt, nt, kt;
-  bool live;
-  TileSrc<BM, BN, kGateUp, kPacked, kGather> src;
-  __device__ void start(const TileWalk<GM>& walk, int logical_, int mt_, int nt_, const int32_t* tiles,
-                        const bf16_t* A, const void* const* W0, const void* const* W1, int K, int N) {
-    logical = logical_, mt = mt_, nt = nt_, kt = 0, live = true;
-    (void)walk;
-    src.setup(tiles, A, W0, W1, K, N, mt, nt);
-  }
-  __device__ void advance(const TileWalk<GM>& walk, const int32_t* tiles, const bf16_t* A, const void* const* W0,
-                          const void* const* W1, int K, int N, int KT) {
-    if (++kt == KT) {
-      kt = 0;
-      logical = walk.seek(logical + walk.G, mt, nt);
-      live = logical < walk.total;
-      if (live) src.setup(tiles, A, W0, W1, K, N, mt, nt);
+// The streaming kernels' persistent walk, with the last round's tiles split
+// along K. After R whole rounds of the G workgroups, L = total mod G tiles
+// are left; run whole, they would hold L compute units for a full tile time
+// while the other G - L idle (measured at the Mixtral-shaped down GEMM: 32
+// tiles left after 8 rounds, 1.5 % of the work, cost 7.8 % of its time).
+// When a partial-sum buffer is given and L <= G / 2, each of those tiles is
+// cut into S = min(G / L, KT / kSplitMinSteps) ranges of K steps; the L * S
+// work units take the last round's slots (one per workgroup), each stores its
+// fp32 accumulators, and split_reduce_kernel sums a tile's S partials in
+// slice order and runs the tile's epilogue. Work items are indexed like
+// tiles: item i < full is logical tile i, item full + u is unit u (tile
+// full + u / S, slice u % S).
+constexpr int kSplitMinSteps = 8;
+constexpr int kSplitUnitFloats = kMfmaBigBM * 256;  // fp32 accumulators of one 256 x 256 tile
+
+template <int GM>
+struct SplitWalk : TileWalk<GM> {
+  int full, S, KT;
+  __device__ SplitWalk(const int32_t* tiles, int capacity, int n_tiles_n, int KT_, bool split, int G_ = 0)
+      : TileWalk<GM>(tiles, capacity, n_tiles_n, G_), full(this->total), S(1), KT(KT_) {
+    if (split) {
+      const int L = this->total % this->G;
+      const int s = (L > 0 && 2 * L <= this->G) ? min(this->G / L, KT / kSplitMinSteps) : 1;
+      if (s >= 2) S = s, full = this->total - L;
     }
   }
+  __device__ int items() const { return full + (this->total - full) * S; }
+  // item `i` (< items()): its tile, K steps [k0, k1) and tail unit (-1: the whole tile)
+  __device__ void item(int i, int& mt, int& nt, int& k0, int& k1, int& unit) const {
+    if (i < full) {
+      this->decode(i, mt, nt);
+      k0 = 0, k1 = KT, unit = -1;
+      return;
+    }
+    const int u = i - full, s = u % S;
+    this->decode(full + u / S, mt, nt);
+    k0 = s * KT / S, k1 = (s + 1) * KT / S, unit = u;
+  }
 };
+
+// Position of a DMA wave in this workgroup's step sequence: the work item
+// and K step it loads next, and that tile's global bases.
+template <int BM, int BN, int GM, bool kGateUp, bool kPacked, bool kGather = false>
+struct StepCursor {
+  int logical, mt, nt, kt, k1, unit;
+  bool live;
+  TileSrc<BM, BN, kGateUp, kPacked, kGather> src;
+  __device__ void start(const SplitWalk<GM>& walk, int logical_, const int32_t* tiles, const bf16_t* A,
+                        const void* const* W0, const void* const* W1, int K, int N) {
+    logical = logical_, live = true;
+    walk.item(logical, mt, nt, kt, k1, unit);
+    src.setup(tiles, A, W0, W1, K, N, mt, nt);
+  }
+  // true when the cursor moved on to the next work item
+  __device__ bool advance(const SplitWalk<GM>& walk, const int32_t* tiles, const bf16_t* A, const void* const* W0,
+                          const void* const* W1, int K, int N) {
+    if (++kt < k1) return false;
+    logical += walk.G;
+    live = logical < walk.items();
+    if (live) {
+      walk.item(logical, mt, nt, kt, k1, unit);
+      src.setup(tiles, A, W0, W1, K, N, mt, nt);
+    }
+    return live;
+  }
+};
+
+// A tail unit's fp32 accumulators, wave by wave in the accumulator layout:
+// part[unit][wave][i][j][lane] as 16-byte vectors (one 1 KB store per wave
+// and 16x16 tile).
+template <int MT16, int NT16>
+__device__ __forceinline__ void store_partial(const f32x4_t (&acc)[MT16][NT16], float* part, int unit, int wave,
+                                              int lane) {
+  f32x4_t* p = reinterpret_cast<f32x4_t*>(part) + ((int64_t)unit * 8 + wave) * (MT16 * NT16 * 64) + lane;
+#pragma unroll
+  for (int i = 0; i < MT16; ++i)
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) p[(i * NT16 + j) * 64] = acc[i][j];
+}
 
 // kGather: A is x and the activation rows are gathered through row_src (the
 // permutation's source tokens).
@@ -381,18 +437,19 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
     int capacity, bf16_t* __restrict__ C, bf16_t* __restrict__ S0, bf16_t* __restrict__ S1,
-    const int32_t* __restrict__ row_src) {
+    const int32_t* __restrict__ row_src, float* __restrict__ part) {
   using Cfg = StreamCfg<kGateUp>;
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
 
-  const TileWalk<Cfg::GM> walk(tiles, capacity, n_tiles_n);
-  int mt = 0, nt = 0;
-  int logical = walk.seek(walk.first_slot(), mt, nt);
-  if (logical >= walk.total) return;
+  const int KT = K / kBK;  // steps per tile
+  // part: partial sums of the split tail tiles (null: the tail runs whole;
+  // only the down GEMMs take one)
+  const SplitWalk<Cfg::GM> walk(tiles, capacity, n_tiles_n, KT, !kGateUp && part != nullptr);
+  int logical = walk.first_slot();
+  if (logical >= walk.items()) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int KT = K / kBK;  // steps per tile
 
   // Global steps g = 0, 1, ... run over this workgroup's tiles back to back.
   // Step g's activations live in A-buffer g % 2 and its weights in B-buffer
@@ -411,8 +468,8 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     auto load_rows = [&]() {
       if constexpr (kGather) grows.load(row_src, ca.src.row0, ca.src.rows, dw * Cfg::OPS, lane, k2);
     };
-    ca.start(walk, logical, mt, nt, tiles, A, W0, W1, K, N);
-    cb.start(walk, logical, mt, nt, tiles, A, W0, W1, K, N);
+    ca.start(walk, logical, tiles, A, W0, W1, K, N);
+    cb.start(walk, logical, tiles, A, W0, W1, K, N);
     load_rows();
     auto issue_a = [&](int buf) {
       const DmaLane dl(lane, ca.kt);
@@ -425,8 +482,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
         else
           ca.src.dma_a(dl, q, k2, base + q * 1024);
       }
-      ca.advance(walk, tiles, A, W0, W1, K, N, KT);
-      if (ca.live && ca.kt == 0) load_rows();  // the next tile's rows
+      if (ca.advance(walk, tiles, A, W0, W1, K, N)) load_rows();  // the next item's rows
     };
     auto issue_b = [&](int buf) {
       const DmaLane dl(lane, cb.kt);
@@ -436,7 +492,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
         const int q = dw * Cfg::OPS + i;
         cb.src.dma_b(dl, lane, cb.kt, q, k2, base + q * 1024);
       }
-      cb.advance(walk, tiles, A, W0, W1, K, N, KT);
+      cb.advance(walk, tiles, A, W0, W1, K, N);
     };
     // prologue in issue order B0, A0, B1, A1, B2 (as far as the steps exist)
     int a_iss = 0, b_iss = 0;
@@ -543,6 +599,8 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
   for (int j = 0; j < NT16; ++j) fb[j] = rdB(vB, 0, j);
 #pragma unroll
   for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
+  int mt = 0, nt = 0, k0 = 0, k1 = 0, unit = -1;
+  walk.item(logical, mt, nt, k0, k1, unit);
   while (true) {
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int t_row0 = ti[1];
@@ -554,20 +612,65 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
     // Every step, a tile's last included, prefetches the first fragments of
-    // the step after it, which is the next tile's first step (its data has
+    // the step after it, which is the next item's first step (its data has
     // landed by X_g; after the workgroup's last step the reads return stale
     // LDS contents that nothing uses). One loop body keeps one register
     // assignment, so the accumulators do not spill at tile boundaries.
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = k0; kt < k1; ++kt) {
       step(std::true_type{});
       rotate();
     }
     __builtin_amdgcn_sched_barrier(0);
-    store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN, kSave>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt, S0,
-                                                                 S1);
-    logical = walk.seek(logical + walk.G, mt, nt);
-    if (logical >= walk.total) break;
+    if (kGateUp || unit < 0)
+      store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN, kSave>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt, S0,
+                                                                   S1);
+    else
+      store_partial(acc, part, unit, wave, lane);
+    logical += walk.G;
+    if (logical >= walk.items()) break;
+    walk.item(logical, mt, nt, k0, k1, unit);
   }
+}
+
+// The epilogue of the split tail tiles (SplitWalk): workgroup t sums the S
+// partials of tail tile t in slice order, wave w taking the accumulators of
+// matrix-core wave w, and stores them as the streaming kernel stores a whole
+// tile. G is the streaming launch's grid; the walk is recomputed from the
+// same tile list, so both kernels agree on which tiles were split.
+template <bool kGateUp, bool kSave>
+__global__ __launch_bounds__(512) void split_reduce_kernel(const float* __restrict__ part,
+                                                           const int32_t* __restrict__ tiles, int capacity,
+                                                           int n_tiles_n, int K, int G,
+                                                           const bf16_t* __restrict__ row_w, bf16_t* __restrict__ C,
+                                                           int N, bf16_t* __restrict__ S0) {
+  using Cfg = StreamCfg<kGateUp>;
+  const SplitWalk<Cfg::GM> walk(tiles, capacity, n_tiles_n, K / kBK, true, G);
+  const int t = blockIdx.x;
+  if (walk.S < 2 || t >= walk.total - walk.full) return;
+  int mt = 0, nt = 0;
+  walk.decode(walk.full + t, mt, nt);
+  const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
+  const int t_row0 = ti[1];
+  const int t_rows = min(Cfg::BM, ti[2] - t_row0);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int MT16 = Cfg::WM / 16, NT16 = Cfg::WN / 16;
+  constexpr int kUnitVecs = kSplitUnitFloats / 4;
+  const f32x4_t* p = reinterpret_cast<const f32x4_t*>(part) + (int64_t)t * walk.S * kUnitVecs +
+                     wave * (MT16 * NT16 * 64) + lane;
+  f32x4_t acc[MT16][NT16];
+#pragma unroll
+  for (int i = 0; i < MT16; ++i)
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) acc[i][j] = p[(i * NT16 + j) * 64];
+  for (int s = 1; s < walk.S; ++s) {
+    const f32x4_t* ps = p + (int64_t)s * kUnitVecs;
+#pragma unroll
+    for (int i = 0; i < MT16; ++i)
+#pragma unroll
+      for (int j = 0; j < NT16; ++j) acc[i][j] += ps[(i * NT16 + j) * 64];
+  }
+  store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN, kSave>(acc, row_w, C, N, wave / Cfg::WGN, wave % Cfg::WGN,
+                                                               t_row0, t_rows, nt, S0, nullptr);
 }
 
 // ===========================================================================
@@ -778,17 +881,28 @@ static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfma
 template <bool kGateUp, bool kPacked, bool kSave = false, bool kGather = false>
 int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
                   const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s, void* S0 = nullptr,
-                  void* S1 = nullptr, const int32_t* row_src = nullptr) {
+                  void* S1 = nullptr, const int32_t* row_src = nullptr, const SplitBuffer& split = {}) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   using Cfg = StreamCfg<kGateUp>;
   const int64_t n_tiles_n = ceil_div(N, kGateUp ? Cfg::BN / 2 : Cfg::BN);  // the last may be partial
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
+  // the down GEMMs' tail can be split when the buffer holds a unit per workgroup
+  float* part = (!kGateUp && split.part != nullptr && split.bytes >= grid * (int64_t)sizeof(float) * kSplitUnitFloats)
+                    ? split.part
+                    : nullptr;
   hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked, kSave, kGather>), dim3((unsigned)grid),
                      dim3(Cfg::THREADS), 0, s, static_cast<const bf16_t*>(A), tiles, W0, W1,
                      static_cast<const bf16_t*>(row_w), (int)K, (int)N, (int)n_tiles_n, (int)capacity,
-                     static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0), static_cast<bf16_t*>(S1), row_src);
-  return check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>");
+                     static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0), static_cast<bf16_t*>(S1), row_src, part);
+  if (int rc = check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>")) return rc;
+  if (part == nullptr) return ASTRAI_MOE_OK;
+  // whether the tail was split is decided on the device (the live tile count
+  // is there): at most G / 2 tail tiles, one workgroup each
+  hipLaunchKernelGGL((split_reduce_kernel<kGateUp, kSave>), dim3((unsigned)((grid + 1) / 2)), dim3(512), 0, s,
+                     part, tiles, (int)capacity, (int)n_tiles_n, (int)K, (int)grid,
+                     static_cast<const bf16_t*>(row_w), static_cast<bf16_t*>(C), (int)N, static_cast<bf16_t*>(S0));
+  return check_launch("split_reduce_kernel");
 }
 
 template <typename Cfg, bool kGateUp, bool kPacked, bool kGather = false>
@@ -818,9 +932,11 @@ int gate_up_dispatch(const void* x_perm, const int32_t* tiles, int64_t capacity,
 
 template <bool kPacked>
 int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
-                  const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, void* y, hipStream_t s) {
+                  const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, void* y, hipStream_t s,
+                  const SplitBuffer& split) {
   if (block_m == kMfmaBigBM)
-    return launch_stream<false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
+    return launch_stream<false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s, nullptr,
+                                         nullptr, nullptr, split);
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
   if (block_m == kMfmaMid2BM)
@@ -854,10 +970,12 @@ int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles, int64_t capaci
 
 int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
                      const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, bool packed, void* y,
-                     hipStream_t s) {
-  return packed ? down_dispatch<true>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s)
-                : down_dispatch<false>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s);
+                     hipStream_t s, const SplitBuffer& split) {
+  return packed ? down_dispatch<true>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s, split)
+                : down_dispatch<false>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s, split);
 }
+
+int64_t split_buffer_bytes() { return (int64_t)cu_count() * (int64_t)sizeof(float) * kSplitUnitFloats; }
 
 int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
                              const void* const* w_up, int64_t dim, int64_t dim_ffn, void* h, void* gu,
@@ -868,9 +986,9 @@ int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles, int64_t c
 
 int launch_mfma_down_save(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
                           const void* sorted_w, int64_t dim_ffn, int64_t dim, void* y, void* y_unweighted,
-                          hipStream_t s) {
+                          hipStream_t s, const SplitBuffer& split) {
   return launch_stream<false, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
-                                           y_unweighted, nullptr);
+                                           y_unweighted, nullptr, nullptr, split);
 }
 
 int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token, const int32_t* tiles, int64_t capacity,

@@ -301,13 +301,27 @@ def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: 
     return h
 
 
+def _split_workspace(h: torch.Tensor, dim: int, block_m: int) -> tuple[torch.Tensor | None, int]:
+    """The down GEMMs' split-tail workspace (fp32 partial sums; see
+    ``astrai_moe_gemm_down``), allocated only where the 256-row matrix-core
+    kernel runs: (tensor or None, bytes)."""
+    if block_m != 256 or h.dtype != torch.bfloat16 or not matrix_core_supported(dim, h.shape[1], h.dtype):
+        return None, 0
+    nbytes = int(loader.library().astrai_moe_gemm_split_bytes())
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=h.device), nbytes
+
+
 def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor | None,
                   n_experts: int, dim: int, block_m: int, out: torch.Tensor | None = None,
-                  packed: bool = False) -> torch.Tensor:
+                  packed: bool = False, split_tail: bool = True) -> torch.Tensor:
     """y = down(h) * routing weight over every expert's rows (mlp.py:24, :97).
 
     ``sorted_w`` None: no routing weight (a dense expert, mlp.py:24 alone).
-    ``packed``: ``w_down`` is a table of packed copies (``moe_pack_down``)."""
+    ``packed``: ``w_down`` is a table of packed copies (``moe_pack_down``).
+    ``split_tail``: the 256-row kernel may split the tiles left after its last
+    whole round of compute units along K (``astrai_moe_gemm_down``); False
+    keeps every tile's single K order, whose bits do not depend on the
+    device's compute-unit count."""
     fn = _kernel("moe_gemm_down")
     _require_gpu(h, "h", 2)
     code = _dtype_code(h, "h")
@@ -319,17 +333,18 @@ def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, so
     _check_tiles(tiles, block_m, h, "moe_gemm_down")
     _require_table(w_down, "w_down", n_experts, h)
     y = _out_buffer(out, n_rows, dim, h)
+    ws, ws_bytes = _split_workspace(h, dim, block_m) if split_tail else (None, 0)
     if packed:
         _check(
             loader.library().astrai_moe_gemm_down_packed(
                 h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), _ptr(sorted_w), code, n_rows,
-                n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
+                n_experts, dim_ffn, dim, block_m, y.data_ptr(), _ptr(ws), ws_bytes, _stream(h)),
             "moe_gemm_down_packed",
         )
         return y
     _check(
         fn(h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(), _ptr(sorted_w), code, n_rows,
-           n_experts, dim_ffn, dim, block_m, y.data_ptr(), _stream(h)),
+           n_experts, dim_ffn, dim, block_m, y.data_ptr(), _ptr(ws), ws_bytes, _stream(h)),
         "moe_gemm_down",
     )
     return y
@@ -531,9 +546,10 @@ def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tens
     _check_tiles(tiles, bm, h, "moe_gemm_down_train")
     _require_table(w_down, "w_down", n_experts, h)
     y, y_unw = (torch.empty(n_rows, dim, dtype=h.dtype, device=h.device) for _ in range(2))
+    ws, ws_bytes = _split_workspace(h, dim, bm)
     _lib_call("astrai_moe_gemm_down_train", h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
               sorted_w.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, bm, y.data_ptr(),
-              y_unw.data_ptr(), _stream(h))
+              y_unw.data_ptr(), _ptr(ws), ws_bytes, _stream(h))
     return y, y_unw
 
 

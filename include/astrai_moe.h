@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 5
+#define ASTRAI_MOE_ABI_VERSION 6
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -222,12 +222,31 @@ int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token,
  *   sorted_w  [n_rows]            dtype, from astrai_moe_permute; NULL for
  *                                 weight 1 (a dense expert: mlp.py:22-25)
  *   y         [n_rows, dim]       dtype
+ *   workspace  fp32 partial sums for the 256-row kernel's last round, or
+ *              NULL; with workspace_bytes >= astrai_moe_gemm_split_bytes()
+ *              the tiles left over after the last whole round of compute
+ *              units (at most half a round) are split along K over all of
+ *              them and summed in a second launch, instead of holding a few
+ *              units for a full tile time while the rest idle. Those tiles'
+ *              fp32 sums then group K differently (within the GEMM tolerance
+ *              of the whole-tile order; deterministic). Not read by other
+ *              tile heights, fp32 or the general kernel. Calls that share a
+ *              workspace must not overlap.
  */
 int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                          int64_t tiles_len, const void* const* w_down,
                          const void* sorted_w, int dtype, int64_t n_rows,
                          int n_experts, int64_t dim_ffn, int64_t dim,
-                         int block_m, void* y, void* stream);
+                         int block_m, void* y, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
+/*
+ * Bytes of the workspace with which astrai_moe_gemm_down (and its packed and
+ * training variants) may split the last round's tiles on the current device:
+ * one 256 x 256 fp32 tile per compute unit (64 MiB on 256 compute units). No
+ * counterpart in the reference (mlp.py:96-98 runs one F.linear per expert).
+ */
+int64_t astrai_moe_gemm_split_bytes(void);
 
 /*
  * Packed expert weights (bf16). No counterpart in the reference: a cached
@@ -275,7 +294,8 @@ int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles,
                                 int64_t tiles_len, const void* const* w_packed,
                                 const void* sorted_w, int dtype, int64_t n_rows,
                                 int n_experts, int64_t dim_ffn, int64_t dim,
-                                int block_m, void* y, void* stream);
+                                int block_m, void* y, void* workspace,
+                                int64_t workspace_bytes, void* stream);
 
 /*
  * Weighted un-permute and combine.
@@ -335,6 +355,7 @@ int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles,
                                const void* sorted_w, int dtype, int64_t n_rows,
                                int n_experts, int64_t dim_ffn, int64_t dim,
                                int block_m, void* y, void* y_unweighted,
+                               void* workspace, int64_t workspace_bytes,
                                void* stream);
 
 /*
