@@ -20,14 +20,19 @@ constexpr int kMfmaMidBM = 64;
 // its weights once where two 64-row tiles would stream them twice.
 constexpr int kMfmaMid2BM = 128;
 
-// Partial-sum buffer of the 256-row kernels' split tail (fp32; none: the last
-// round's tiles run whole). split_buffer_bytes() lets every launch on the
-// current device split: one 256 x 256 fp32 tile per compute unit.
-struct SplitBuffer {
-  float* part = nullptr;
+// Scratch of the 256-row streaming kernels (none: every work item is dealt
+// statically and the tiles left over after the last whole round run whole).
+// The first kSchedBytes hold the run-time work claims (a counter the launch
+// clears, and one mailbox ring per workgroup); the down GEMMs' split-tail
+// partial sums follow, one 256 x 256 fp32 tile per workgroup.
+// gemm_workspace_bytes(down) is the size that enables both on the current
+// device.
+struct GemmWorkspace {
+  void* base = nullptr;
   int64_t bytes = 0;
 };
-int64_t split_buffer_bytes();
+constexpr int64_t kSchedBytes = 65536;
+int64_t gemm_workspace_bytes(bool down);
 
 // Shape constraints of the bf16 kernels: K a multiple of 64, the output
 // columns a multiple of the column tile, 16-byte aligned operands.
@@ -41,12 +46,13 @@ bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m,
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles,
                         int64_t capacity, const void* const* w_gate,
                         const void* const* w_up, int64_t dim, int64_t dim_ffn,
-                        int block_m, bool packed, void* h, hipStream_t s);
+                        int block_m, bool packed, void* h, hipStream_t s,
+                        const GemmWorkspace& ws = {});
 int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity,
                      const void* const* w_down, const void* sorted_w,
                      int64_t dim_ffn, int64_t dim, int block_m, bool packed,
                      void* y, hipStream_t s,
-                     const SplitBuffer& split = {});
+                     const GemmWorkspace& ws = {});
 
 // As launch_mfma_gate_up, reading the activation rows as x[sorted_token[r]]
 // (x: [n_tokens, dim]) instead of a copied x_perm.
@@ -55,7 +61,8 @@ int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token,
                                const void* const* w_gate,
                                const void* const* w_up, int64_t dim,
                                int64_t dim_ffn, int block_m, void* h,
-                               hipStream_t s);
+                               hipStream_t s,
+                        const GemmWorkspace& ws = {});
 
 // Training forward (256-row tiles): as launch_mfma_gate_up / launch_mfma_down,
 // also storing the bf16 gate and up projections (gu: [rows, 2 dim_ffn],
@@ -65,12 +72,13 @@ int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles,
                              int64_t capacity, const void* const* w_gate,
                              const void* const* w_up, int64_t dim,
                              int64_t dim_ffn, void* h, void* gu,
-                             hipStream_t s);
+                             hipStream_t s,
+                        const GemmWorkspace& ws = {});
 int launch_mfma_down_save(const void* h, const int32_t* tiles,
                           int64_t capacity, const void* const* w_down,
                           const void* sorted_w, int64_t dim_ffn, int64_t dim,
                           void* y, void* y_unweighted, hipStream_t s,
-                          const SplitBuffer& split = {});
+                          const GemmWorkspace& ws = {});
 
 // fp32 on the matrix cores (moe_gemm_mfma_f32.hip), 64-row tile lists, K a
 // multiple of 32, output columns a multiple of 32 (gate/up) or 64 (down),

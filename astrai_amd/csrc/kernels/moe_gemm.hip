@@ -169,10 +169,10 @@ int check_common(const char* who, const void* A, const int32_t* tiles,
   return ASTRAI_MOE_OK;
 }
 
-// The split-tail workspace: optional; when given, 16-byte aligned with a
-// non-negative size (a size below astrai_moe_gemm_split_bytes() leaves the
-// tail whole).
-int check_split(const char* who, const void* workspace, int64_t workspace_bytes) {
+// The GEMM workspace: optional; when given, 16-byte aligned with a
+// non-negative size (one smaller than astrai_moe_gemm_workspace_bytes()
+// gives turns the run-time claims or the split tail off).
+int check_workspace(const char* who, const void* workspace, int64_t workspace_bytes) {
   ASTRAI_REQUIRE(workspace_bytes >= 0, "%s: negative workspace size %lld", who, (long long)workspace_bytes);
   ASTRAI_REQUIRE(workspace == nullptr || reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
                  "%s: workspace must be 16-byte aligned", who);
@@ -190,11 +190,13 @@ extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
                                        const void* const* w_up, int dtype,
                                        int64_t n_rows, int n_experts,
                                        int64_t dim, int64_t dim_ffn,
-                                       int block_m, void* h, void* stream) {
+                                       int block_m, void* h, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
   clear_error();
   int rc = check_common("gemm_gate_up", x_perm, tiles, tiles_len, dtype, n_rows,
                         n_experts, dim, dim_ffn, block_m, h);
   if (rc) return rc;
+  if ((rc = check_workspace("gemm_gate_up", workspace, workspace_bytes))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_gate && w_up, "gemm_gate_up: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
@@ -202,7 +204,8 @@ extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
   if (dtype == ASTRAI_MOE_BF16) {
     if (mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h))
       return launch_mfma_gate_up(x_perm, tiles, capacity, w_gate, w_up, dim,
-                                 dim_ffn, block_m, false, h, s);
+                                 dim_ffn, block_m, false, h, s,
+                                 GemmWorkspace{workspace, workspace_bytes});
     return launch_generic<bf16_t, true>(x_perm, tiles, capacity, w_gate, w_up,
                                         nullptr, dim, dim_ffn, h, s);
   }
@@ -216,11 +219,13 @@ extern "C" int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
 extern "C" int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token, int64_t n_tokens,
                                               const int32_t* tiles, int64_t tiles_len, const void* const* w_gate,
                                               const void* const* w_up, int dtype, int64_t n_rows, int n_experts,
-                                              int64_t dim, int64_t dim_ffn, int block_m, void* h, void* stream) {
+                                              int64_t dim, int64_t dim_ffn, int block_m, void* h, void* workspace,
+                                              int64_t workspace_bytes, void* stream) {
   clear_error();
   int rc = check_common("gemm_gate_up_gather", x, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn, block_m,
                         h);
   if (rc) return rc;
+  if ((rc = check_workspace("gemm_gate_up_gather", workspace, workspace_bytes))) return rc;
   ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_gate_up_gather: bf16 only (dtype %d)", dtype);
   ASTRAI_REQUIRE(n_tokens >= 0 && n_tokens * dim * 2 < (1ll << 32),
                  "gemm_gate_up_gather: x must be under 4 GiB (n_tokens %lld, dim %lld)", (long long)n_tokens,
@@ -232,7 +237,7 @@ extern "C" int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sort
   ASTRAI_REQUIRE(sorted_token && w_gate && w_up, "gemm_gate_up_gather: null row list or weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   return launch_mfma_gate_up_gather(x, sorted_token, tiles, capacity, w_gate, w_up, dim, dim_ffn, block_m, h,
-                                    static_cast<hipStream_t>(stream));
+                                    static_cast<hipStream_t>(stream), GemmWorkspace{workspace, workspace_bytes});
 }
 
 extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
@@ -247,7 +252,7 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
   int rc = check_common("gemm_down", h, tiles, tiles_len, dtype, n_rows,
                         n_experts, dim_ffn, dim, block_m, y);
   if (rc) return rc;
-  if ((rc = check_split("gemm_down", workspace, workspace_bytes))) return rc;
+  if ((rc = check_workspace("gemm_down", workspace, workspace_bytes))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_down, "gemm_down: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
@@ -256,7 +261,7 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
     if (mfma_down_supported(dim_ffn, dim, block_m, h, y))
       return launch_mfma_down(h, tiles, capacity, w_down, sorted_w, dim_ffn,
                               dim, block_m, false, y, s,
-                              SplitBuffer{static_cast<float*>(workspace), workspace_bytes});
+                              GemmWorkspace{workspace, workspace_bytes});
     return launch_generic<bf16_t, false>(h, tiles, capacity, w_down, nullptr,
                                          sorted_w, dim_ffn, dim, y, s);
   }
@@ -267,7 +272,7 @@ extern "C" int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                                       sorted_w, dim_ffn, dim, y, s);
 }
 
-extern "C" int64_t astrai_moe_gemm_split_bytes(void) { return split_buffer_bytes(); }
+extern "C" int64_t astrai_moe_gemm_workspace_bytes(int down) { return gemm_workspace_bytes(down != 0); }
 
 static bool aligned16_ptr(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
@@ -300,11 +305,12 @@ extern "C" int astrai_moe_pack_down(const void* w_down, int dtype, int64_t dim,
 extern "C" int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t* tiles, int64_t tiles_len,
                                               const void* const* w_packed, int dtype, int64_t n_rows,
                                               int n_experts, int64_t dim, int64_t dim_ffn, int block_m, void* h,
-                                              void* stream) {
+                                              void* workspace, int64_t workspace_bytes, void* stream) {
   clear_error();
   int rc = check_common("gemm_gate_up_packed", x_perm, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn,
                         block_m, h);
   if (rc) return rc;
+  if ((rc = check_workspace("gemm_gate_up_packed", workspace, workspace_bytes))) return rc;
   ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_gate_up_packed: packed weights are bf16 only");
   // packed weights come in whole 256-row tiles (128 gate + 128 up rows)
   ASTRAI_REQUIRE(n_rows == 0 || (dim_ffn % 128 == 0 && mfma_gate_up_supported(dim, dim_ffn, block_m, x_perm, h)),
@@ -314,7 +320,7 @@ extern "C" int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t*
   ASTRAI_REQUIRE(w_packed, "gemm_gate_up_packed: null weight table");
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   return launch_mfma_gate_up(x_perm, tiles, capacity, w_packed, w_packed, dim, dim_ffn, block_m, true, h,
-                             static_cast<hipStream_t>(stream));
+                             static_cast<hipStream_t>(stream), GemmWorkspace{workspace, workspace_bytes});
 }
 
 extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, int64_t tiles_len,
@@ -326,7 +332,7 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
   int rc = check_common("gemm_down_packed", h, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m,
                         y);
   if (rc) return rc;
-  if ((rc = check_split("gemm_down_packed", workspace, workspace_bytes))) return rc;
+  if ((rc = check_workspace("gemm_down_packed", workspace, workspace_bytes))) return rc;
   ASTRAI_REQUIRE(dtype == ASTRAI_MOE_BF16, "gemm_down_packed: packed weights are bf16 only");
   ASTRAI_REQUIRE(n_rows == 0 || (dim % 256 == 0 && mfma_down_supported(dim_ffn, dim, block_m, h, y)),
                  "gemm_down_packed: unsupported shape (dim_ffn %lld, dim %lld, block_m %d) or alignment",
@@ -336,7 +342,7 @@ extern "C" int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles, 
   const int64_t capacity = (tiles_len - ASTRAI_MOE_TILE_HEADER) / ASTRAI_MOE_TILE_STRIDE;
   return launch_mfma_down(h, tiles, capacity, w_packed, sorted_w, dim_ffn, dim, block_m, true, y,
                           static_cast<hipStream_t>(stream),
-                          SplitBuffer{static_cast<float*>(workspace), workspace_bytes});
+                          GemmWorkspace{workspace, workspace_bytes});
 }
 
 // ---------------------------------------------------------------------------
@@ -363,11 +369,13 @@ static int check_train(const char* who, int dtype, int64_t dim, int64_t dim_ffn,
 extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles, int64_t tiles_len,
                                              const void* const* w_gate, const void* const* w_up, int dtype,
                                              int64_t n_rows, int n_experts, int64_t dim, int64_t dim_ffn,
-                                             int block_m, void* h, void* gu, void* stream) {
+                                             int block_m, void* h, void* gu, void* workspace,
+                                             int64_t workspace_bytes, void* stream) {
   clear_error();
   int rc = check_common("gemm_gate_up_train", x_perm, tiles, tiles_len, dtype, n_rows, n_experts, dim, dim_ffn,
                         block_m, h);
   if (rc) return rc;
+  if ((rc = check_workspace("gemm_gate_up_train", workspace, workspace_bytes))) return rc;
   if ((rc = check_train("gemm_gate_up_train", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_gate && w_up && gu, "gemm_gate_up_train: null weight table or output");
@@ -376,7 +384,8 @@ extern "C" int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* 
   if (mfma_train_shape(dtype, dim, dim_ffn)) {
     ASTRAI_REQUIRE(aligned16_ptr(x_perm) && aligned16_ptr(h) && aligned16_ptr(gu),
                    "gemm_gate_up_train: buffers must be 16-byte aligned");
-    return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, gu, s);
+    return launch_mfma_gate_up_save(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, h, gu, s,
+                                    GemmWorkspace{workspace, workspace_bytes});
   }
   if (dtype == ASTRAI_MOE_BF16)
     return launch_generic<bf16_t, true, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
@@ -394,7 +403,7 @@ extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, i
   clear_error();
   int rc = check_common("gemm_down_train", h, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m, y);
   if (rc) return rc;
-  if ((rc = check_split("gemm_down_train", workspace, workspace_bytes))) return rc;
+  if ((rc = check_workspace("gemm_down_train", workspace, workspace_bytes))) return rc;
   if ((rc = check_train("gemm_down_train", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(w_down && sorted_w && y_unweighted, "gemm_down_train: null weight table, row weights or output");
@@ -404,7 +413,7 @@ extern "C" int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles, i
     ASTRAI_REQUIRE(aligned16_ptr(h) && aligned16_ptr(y) && aligned16_ptr(y_unweighted),
                    "gemm_down_train: buffers must be 16-byte aligned");
     return launch_mfma_down_save(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, y, y_unweighted, s,
-                                 SplitBuffer{static_cast<float*>(workspace), workspace_bytes});
+                                 GemmWorkspace{workspace, workspace_bytes});
   }
   if (dtype == ASTRAI_MOE_BF16)
     return launch_generic<bf16_t, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,

@@ -390,29 +390,92 @@ struct SplitWalk : TileWalk<GM> {
   }
 };
 
+// The order in which one workgroup takes its work items. Items below `dyn`
+// are dealt statically: the workgroup's slot, then every G-th item. Given a
+// scheduling block (`sched`, its counter cleared before the launch), the
+// items from `dyn` on are claimed at run time from the counter sched[0] by
+// whichever workgroups get there first, so that the compute units running at
+// a higher clock take more of them (the XCDs of one part hold clocks several
+// per cent apart under this load, and with a static deal the slowest one sets
+// the kernel's end). Matrix-core wave 0 claims a workgroup's next item
+// kClaimLead steps before the end of its current one and publishes it in the
+// workgroup's ring of 8 mailbox slots (sched[kMailboxBase + 8 b ...]); every
+// wave reads it when it leaves the current item, at least two barriers
+// after the store (the DMA waves run up to three steps ahead of the
+// matrix-core waves). -1: no item. Claiming that late needs every dynamic
+// item to last more than kClaimLead steps. A claim stalls its workgroup for
+// about an atomic's round trip, so claims are made only where tiles are long
+// (kDynamicMinSteps): measured against the static deal, in one process with
+// the builds alternating, the Mixtral-shaped GEMMs (64 and 224 steps per
+// tile) gained 1.8 % (gate/up) and 0.8 % (down), while the fine-grained
+// shape (32 and 22 steps) lost 0.4 % and 2.4 %.
+constexpr int kMailboxBase = 64;       // int32 offset of the mailboxes in the scheduling block
+constexpr int kMaxSchedGroups = 1024;  // workgroups the scheduling block has mailboxes for
+constexpr int kDynamicShare = 10;      // 1 / kDynamicShare of the items are claimed at run time
+constexpr int kDynamicMinSteps = 48;   // K steps per tile from which items are claimed at run time
+constexpr int kClaimLead = 6;
+static_assert(kClaimLead > 4 && kClaimLead < kSplitMinSteps, "claim between the DMA waves' lead and an item's end");
+
+struct ItemSeq {
+  int slot, G, m, n, dyn;
+  int* mbox;  // the workgroup's 8 mailbox slots (nullptr: static deal only)
+  template <int GM>
+  __device__ ItemSeq(const SplitWalk<GM>& walk, int KT, int* sched)
+      : slot(walk.first_slot()), G(walk.G), n(walk.items()), dyn(walk.items()), mbox(nullptr) {
+    if (sched != nullptr && KT >= kDynamicMinSteps && G <= kMaxSchedGroups) {
+      const int d = max(G, n - n / kDynamicShare);
+      if (d < n) dyn = d, mbox = sched + kMailboxBase + 8 * (int)blockIdx.x;
+    }
+    m = slot < dyn ? (dyn - slot + G - 1) / G : 0;
+  }
+  // the workgroup's item `idx` (a mailbox read for the claimed ones)
+  __device__ int id(int idx) const {
+    if (idx < m) return slot + idx * G;
+    if (mbox == nullptr) return -1;
+    return __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(mbox + ((idx - m) & 7), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  }
+  // whether the item after `idx` is claimed at run time
+  __device__ bool claims_next(int idx) const { return mbox != nullptr && idx + 1 >= m; }
+  // matrix-core wave 0, kClaimLead steps before the end of item `idx`:
+  // claims the next item; false once a claim came back empty
+  __device__ bool claim(int idx, int* sched) const {
+    int c = 0;
+    if (__lane_id() == 0) c = __hip_atomic_fetch_add(sched, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    c = __builtin_amdgcn_readfirstlane(c);
+    const int v = dyn + c < n ? dyn + c : -1;
+    if (__lane_id() == 0)
+      __hip_atomic_store(mbox + ((idx + 1 - m) & 7), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the store lands in L2 before this wave's next barrier
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return v >= 0;
+  }
+};
+
 // Position of a DMA wave in this workgroup's step sequence: the work item
 // and K step it loads next, and that tile's global bases.
 template <int BM, int BN, int GM, bool kGateUp, bool kPacked, bool kGather = false>
 struct StepCursor {
-  int logical, mt, nt, kt, k1, unit;
+  int idx, mt, nt, kt, k1, unit;  // idx: the item's place in the workgroup's order
   bool live;
   TileSrc<BM, BN, kGateUp, kPacked, kGather> src;
-  __device__ void start(const SplitWalk<GM>& walk, int logical_, const int32_t* tiles, const bf16_t* A,
+  __device__ void enter(const SplitWalk<GM>& walk, int logical, const int32_t* tiles, const bf16_t* A,
                         const void* const* W0, const void* const* W1, int K, int N) {
-    logical = logical_, live = true;
     walk.item(logical, mt, nt, kt, k1, unit);
     src.setup(tiles, A, W0, W1, K, N, mt, nt);
   }
+  __device__ void start(const SplitWalk<GM>& walk, const ItemSeq& seq, const int32_t* tiles, const bf16_t* A,
+                        const void* const* W0, const void* const* W1, int K, int N) {
+    idx = 0, live = true;
+    enter(walk, seq.id(0), tiles, A, W0, W1, K, N);
+  }
   // true when the cursor moved on to the next work item
-  __device__ bool advance(const SplitWalk<GM>& walk, const int32_t* tiles, const bf16_t* A, const void* const* W0,
-                          const void* const* W1, int K, int N) {
+  __device__ bool advance(const SplitWalk<GM>& walk, const ItemSeq& seq, const int32_t* tiles, const bf16_t* A,
+                          const void* const* W0, const void* const* W1, int K, int N) {
     if (++kt < k1) return false;
-    logical += walk.G;
-    live = logical < walk.items();
-    if (live) {
-      walk.item(logical, mt, nt, kt, k1, unit);
-      src.setup(tiles, A, W0, W1, K, N, mt, nt);
-    }
+    const int nxt = seq.id(++idx);  // a claimed item was published two barriers ago
+    live = nxt >= 0;
+    if (live) enter(walk, nxt, tiles, A, W0, W1, K, N);
     return live;
   }
 };
@@ -437,16 +500,17 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     const bf16_t* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W0,
     const void* const* __restrict__ W1, const bf16_t* __restrict__ row_w, int K, int N, int n_tiles_n,
     int capacity, bf16_t* __restrict__ C, bf16_t* __restrict__ S0, bf16_t* __restrict__ S1,
-    const int32_t* __restrict__ row_src, float* __restrict__ part) {
+    const int32_t* __restrict__ row_src, float* __restrict__ part, int32_t* __restrict__ sched) {
   using Cfg = StreamCfg<kGateUp>;
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
 
   const int KT = K / kBK;  // steps per tile
   // part: partial sums of the split tail tiles (null: the tail runs whole;
-  // only the down GEMMs take one)
+  // only the down GEMMs take one); sched: the run-time claims (null: the
+  // whole walk is dealt statically)
   const SplitWalk<Cfg::GM> walk(tiles, capacity, n_tiles_n, KT, !kGateUp && part != nullptr);
-  int logical = walk.first_slot();
-  if (logical >= walk.items()) return;
+  const ItemSeq seq(walk, KT, sched);
+  if (seq.m == 0) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -468,8 +532,8 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     auto load_rows = [&]() {
       if constexpr (kGather) grows.load(row_src, ca.src.row0, ca.src.rows, dw * Cfg::OPS, lane, k2);
     };
-    ca.start(walk, logical, tiles, A, W0, W1, K, N);
-    cb.start(walk, logical, tiles, A, W0, W1, K, N);
+    ca.start(walk, seq, tiles, A, W0, W1, K, N);
+    cb.start(walk, seq, tiles, A, W0, W1, K, N);
     load_rows();
     auto issue_a = [&](int buf) {
       const DmaLane dl(lane, ca.kt);
@@ -482,7 +546,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
         else
           ca.src.dma_a(dl, q, k2, base + q * 1024);
       }
-      if (ca.advance(walk, tiles, A, W0, W1, K, N)) load_rows();  // the next item's rows
+      if (ca.advance(walk, seq, tiles, A, W0, W1, K, N)) load_rows();  // the next item's rows
     };
     auto issue_b = [&](int buf) {
       const DmaLane dl(lane, cb.kt);
@@ -492,7 +556,7 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
         const int q = dw * Cfg::OPS + i;
         cb.src.dma_b(dl, lane, cb.kt, q, k2, base + q * 1024);
       }
-      cb.advance(walk, tiles, A, W0, W1, K, N);
+      cb.advance(walk, seq, tiles, A, W0, W1, K, N);
     };
     // prologue in issue order B0, A0, B1, A1, B2 (as far as the steps exist)
     int a_iss = 0, b_iss = 0;
@@ -600,8 +664,10 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
 #pragma unroll
   for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
   int mt = 0, nt = 0, k0 = 0, k1 = 0, unit = -1;
-  walk.item(logical, mt, nt, k0, k1, unit);
-  while (true) {
+  bool claiming = wave == 0;  // matrix-core wave 0 makes the run-time claims
+  walk.item(seq.id(0), mt, nt, k0, k1, unit);
+  for (int idx = 0;; ++idx) {
+    const int claim_at = (claiming && seq.claims_next(idx)) ? k1 - kClaimLead : -1;
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int t_row0 = ti[1];
     const int t_rows = min(Cfg::BM, ti[2] - t_row0);
@@ -616,19 +682,25 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     // landed by X_g; after the workgroup's last step the reads return stale
     // LDS contents that nothing uses). One loop body keeps one register
     // assignment, so the accumulators do not spill at tile boundaries.
-    for (int kt = k0; kt < k1; ++kt) {
-      step(std::true_type{});
-      rotate();
+    // the K loop runs in two stretches around the claim, so that the loop
+    // body itself carries nothing for it
+    for (int kt = k0, stop = claim_at >= 0 ? claim_at : k1;; stop = k1) {
+      for (; kt < stop; ++kt) {
+        step(std::true_type{});
+        rotate();
+      }
+      if (kt == k1) break;
+      claiming = seq.claim(idx, sched);
     }
     __builtin_amdgcn_sched_barrier(0);
+    const int nxt = seq.id(idx + 1);
     if (kGateUp || unit < 0)
       store_tile_direct<kGateUp, Cfg::WM, Cfg::WN, Cfg::BN, kSave>(acc, row_w, C, N, wm, wn, t_row0, t_rows, nt, S0,
                                                                    S1);
     else
       store_partial(acc, part, unit, wave, lane);
-    logical += walk.G;
-    if (logical >= walk.items()) break;
-    walk.item(logical, mt, nt, k0, k1, unit);
+    if (nxt < 0) break;
+    walk.item(nxt, mt, nt, k0, k1, unit);
   }
 }
 
@@ -878,23 +950,40 @@ using MidCfg = TileCfg<kMfmaMidBM, 256, 3, 2, 4, 8>;
 using Mid2Cfg = TileCfg<kMfmaMid2BM, 256, 3, 1, 8, 8>;
 static_assert(StreamCfg<true>::BM == kMfmaBigBM && StreamCfg<false>::BM == kMfmaBigBM, "prefill tile height");
 
+// Clears the run-time claim counter of a streaming launch's scheduling
+// block (enqueued right before it, so the caller's workspace needs no
+// initialisation and a captured graph clears it on every replay).
+__global__ __launch_bounds__(64) void sched_clear_kernel(int32_t* __restrict__ sched) {
+  if (threadIdx.x == 0) sched[0] = 0;
+}
+
 template <bool kGateUp, bool kPacked, bool kSave = false, bool kGather = false>
 int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const void* const* W0, const void* const* W1,
                   const void* row_w, int64_t K, int64_t N, void* C, hipStream_t s, void* S0 = nullptr,
-                  void* S1 = nullptr, const int32_t* row_src = nullptr, const SplitBuffer& split = {}) {
+                  void* S1 = nullptr, const int32_t* row_src = nullptr, const GemmWorkspace& ws = {}) {
   if (capacity == 0) return ASTRAI_MOE_OK;
   using Cfg = StreamCfg<kGateUp>;
   const int64_t n_tiles_n = ceil_div(N, kGateUp ? Cfg::BN / 2 : Cfg::BN);  // the last may be partial
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  // the down GEMMs' tail can be split when the buffer holds a unit per workgroup
-  float* part = (!kGateUp && split.part != nullptr && split.bytes >= grid * (int64_t)sizeof(float) * kSplitUnitFloats)
-                    ? split.part
+  // run-time claims need the scheduling block; the down GEMMs' tail can be
+  // split when the partial sums hold a unit per workgroup
+  int32_t* sched = (ws.base != nullptr && ws.bytes >= kSchedBytes && grid <= kMaxSchedGroups)
+                       ? static_cast<int32_t*>(ws.base)
+                       : nullptr;
+  float* part = (!kGateUp && sched != nullptr &&
+                 ws.bytes >= kSchedBytes + grid * (int64_t)sizeof(float) * kSplitUnitFloats)
+                    ? reinterpret_cast<float*>(static_cast<char*>(ws.base) + kSchedBytes)
                     : nullptr;
+  if (sched != nullptr) {
+    hipLaunchKernelGGL(sched_clear_kernel, dim3(1), dim3(64), 0, s, sched);
+    if (int rc = check_launch("sched_clear_kernel")) return rc;
+  }
   hipLaunchKernelGGL((gemm_stream_kernel<kGateUp, kPacked, kSave, kGather>), dim3((unsigned)grid),
                      dim3(Cfg::THREADS), 0, s, static_cast<const bf16_t*>(A), tiles, W0, W1,
                      static_cast<const bf16_t*>(row_w), (int)K, (int)N, (int)n_tiles_n, (int)capacity,
-                     static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0), static_cast<bf16_t*>(S1), row_src, part);
+                     static_cast<bf16_t*>(C), static_cast<bf16_t*>(S0), static_cast<bf16_t*>(S1), row_src, part,
+                     sched);
   if (int rc = check_launch(kGateUp ? "gemm_stream_kernel<gate_up>" : "gemm_stream_kernel<down>")) return rc;
   if (part == nullptr) return ASTRAI_MOE_OK;
   // whether the tail was split is decided on the device (the live tile count
@@ -920,9 +1009,11 @@ int launch(const void* A, const int32_t* tiles, int64_t capacity, const void* co
 
 template <bool kPacked>
 int gate_up_dispatch(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
-                     const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, void* h, hipStream_t s) {
+                     const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, void* h, hipStream_t s,
+                     const GemmWorkspace& ws) {
   if (block_m == kMfmaBigBM)
-    return launch_stream<true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
+    return launch_stream<true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, nullptr,
+                                        nullptr, nullptr, ws);
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, true, kPacked>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s);
   if (block_m == kMfmaMid2BM)
@@ -933,10 +1024,10 @@ int gate_up_dispatch(const void* x_perm, const int32_t* tiles, int64_t capacity,
 template <bool kPacked>
 int down_dispatch(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
                   const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, void* y, hipStream_t s,
-                  const SplitBuffer& split) {
+                  const GemmWorkspace& ws) {
   if (block_m == kMfmaBigBM)
     return launch_stream<false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s, nullptr,
-                                         nullptr, nullptr, split);
+                                         nullptr, nullptr, ws);
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, false, kPacked>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s);
   if (block_m == kMfmaMid2BM)
@@ -963,40 +1054,42 @@ bool mfma_down_supported(int64_t dim_ffn, int64_t dim, int block_m, const void* 
 
 int launch_mfma_gate_up(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
                         const void* const* w_up, int64_t dim, int64_t dim_ffn, int block_m, bool packed, void* h,
-                        hipStream_t s) {
-  return packed ? gate_up_dispatch<true>(x_perm, tiles, capacity, w_gate, w_gate, dim, dim_ffn, block_m, h, s)
-                : gate_up_dispatch<false>(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, block_m, h, s);
+                        hipStream_t s, const GemmWorkspace& ws) {
+  return packed ? gate_up_dispatch<true>(x_perm, tiles, capacity, w_gate, w_gate, dim, dim_ffn, block_m, h, s, ws)
+                : gate_up_dispatch<false>(x_perm, tiles, capacity, w_gate, w_up, dim, dim_ffn, block_m, h, s, ws);
 }
 
 int launch_mfma_down(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
                      const void* sorted_w, int64_t dim_ffn, int64_t dim, int block_m, bool packed, void* y,
-                     hipStream_t s, const SplitBuffer& split) {
-  return packed ? down_dispatch<true>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s, split)
-                : down_dispatch<false>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s, split);
+                     hipStream_t s, const GemmWorkspace& ws) {
+  return packed ? down_dispatch<true>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s, ws)
+                : down_dispatch<false>(h, tiles, capacity, w_down, sorted_w, dim_ffn, dim, block_m, y, s, ws);
 }
 
-int64_t split_buffer_bytes() { return (int64_t)cu_count() * (int64_t)sizeof(float) * kSplitUnitFloats; }
+int64_t gemm_workspace_bytes(bool down) {
+  return kSchedBytes + (down ? (int64_t)cu_count() * (int64_t)sizeof(float) * kSplitUnitFloats : 0);
+}
 
 int launch_mfma_gate_up_save(const void* x_perm, const int32_t* tiles, int64_t capacity, const void* const* w_gate,
                              const void* const* w_up, int64_t dim, int64_t dim_ffn, void* h, void* gu,
-                             hipStream_t s) {
+                             hipStream_t s, const GemmWorkspace& ws) {
   return launch_stream<true, false, true>(x_perm, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s, gu,
-                                          nullptr);
+                                          nullptr, nullptr, ws);
 }
 
 int launch_mfma_down_save(const void* h, const int32_t* tiles, int64_t capacity, const void* const* w_down,
                           const void* sorted_w, int64_t dim_ffn, int64_t dim, void* y, void* y_unweighted,
-                          hipStream_t s, const SplitBuffer& split) {
+                          hipStream_t s, const GemmWorkspace& ws) {
   return launch_stream<false, false, true>(h, tiles, capacity, w_down, nullptr, sorted_w, dim_ffn, dim, y, s,
-                                           y_unweighted, nullptr, nullptr, split);
+                                           y_unweighted, nullptr, nullptr, ws);
 }
 
 int launch_mfma_gate_up_gather(const void* x, const int32_t* sorted_token, const int32_t* tiles, int64_t capacity,
                                const void* const* w_gate, const void* const* w_up, int64_t dim, int64_t dim_ffn,
-                               int block_m, void* h, hipStream_t s) {
+                               int block_m, void* h, hipStream_t s, const GemmWorkspace& ws) {
   if (block_m == kMfmaBigBM)
     return launch_stream<true, false, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
-                                                   nullptr, nullptr, sorted_token);
+                                                   nullptr, nullptr, sorted_token, ws);
   if (block_m == kMfmaMidBM)
     return launch<MidCfg, true, false, true>(x, tiles, capacity, w_gate, w_up, nullptr, dim, dim_ffn, h, s,
                                              sorted_token);

@@ -226,12 +226,28 @@ def moe_permute(route: RouteResult, x: torch.Tensor, n_experts: int, block_m: in
     return PermuteResult(offsets, sorted_token, sorted_w, token_pos, x_perm, _tag_tiles(tiles, block_m), block_m)
 
 
+def _workspace(a: torch.Tensor, dim: int, dim_ffn: int, block_m: int, down: bool,
+               balance: bool = True) -> tuple[torch.Tensor | None, int]:
+    """Scratch of the 256-row matrix-core GEMMs (``astrai_moe_gemm_gate_up``,
+    ``astrai_moe_gemm_down``): the run-time claims of the last tenth of the
+    work and, for the down GEMMs, the partial sums of the split last round.
+    Allocated only where that kernel runs: (tensor or None, bytes).
+    ``balance=False``: none, every tile dealt in advance and run whole."""
+    if not balance or block_m != 256 or a.dtype != torch.bfloat16 or not matrix_core_supported(dim, dim_ffn, a.dtype):
+        return None, 0
+    nbytes = int(loader.library().astrai_moe_gemm_workspace_bytes(1 if down else 0))
+    return torch.empty(nbytes, dtype=torch.uint8, device=a.device), nbytes
+
+
 def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
-                     n_experts: int, dim_ffn: int, block_m: int, packed: bool = False) -> torch.Tensor:
+                     n_experts: int, dim_ffn: int, block_m: int, packed: bool = False,
+                     balance: bool = True) -> torch.Tensor:
     """h = up(x) * silu(gate(x)) over every expert's rows (mlp.py:22-23).
 
     ``packed``: ``w_gate`` is a table of packed gate/up copies
-    (``moe_pack_gate_up``) and ``w_up`` is ignored; same results."""
+    (``moe_pack_gate_up``) and ``w_up`` is ignored; same results.
+    ``balance``: the 256-row kernel may hand out the last tenth of its tiles
+    at run time (same results; False deals every tile in advance)."""
     fn = _kernel("moe_gemm_gate_up")
     _require_gpu(x_perm, "x_perm", 2)
     code = _dtype_code(x_perm, "x_perm")
@@ -241,17 +257,18 @@ def moe_gemm_gate_up(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Te
     if not packed:
         _require_table(w_up, "w_up", n_experts, x_perm)
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
+    ws, ws_bytes = _workspace(x_perm, dim, dim_ffn, block_m, down=False, balance=balance)
     if packed:
         _check(
             loader.library().astrai_moe_gemm_gate_up_packed(
                 x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(), code, n_rows, n_experts, dim,
-                dim_ffn, block_m, h.data_ptr(), _stream(x_perm)),
+                dim_ffn, block_m, h.data_ptr(), _ptr(ws), ws_bytes, _stream(x_perm)),
             "moe_gemm_gate_up_packed",
         )
         return h
     _check(
         fn(x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(), w_up.data_ptr(), code, n_rows,
-           n_experts, dim, dim_ffn, block_m, h.data_ptr(), _stream(x_perm)),
+           n_experts, dim, dim_ffn, block_m, h.data_ptr(), _ptr(ws), ws_bytes, _stream(x_perm)),
         "moe_gemm_gate_up",
     )
     return h
@@ -281,7 +298,8 @@ def gather_supported(n_tokens: int, dim: int, dim_ffn: int, dtype: torch.dtype) 
 
 
 def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor,
-                            w_up: torch.Tensor, n_experts: int, dim_ffn: int, block_m: int) -> torch.Tensor:
+                            w_up: torch.Tensor, n_experts: int, dim_ffn: int, block_m: int,
+                            balance: bool = True) -> torch.Tensor:
     """``moe_gemm_gate_up`` on the permuted rows ``x[sorted_token]`` read
     straight from ``x`` (no copied ``x_perm``); bit-identical results."""
     _require_gpu(x, "x", 2)
@@ -292,36 +310,29 @@ def moe_gemm_gate_up_gather(x: torch.Tensor, sorted_token: torch.Tensor, tiles: 
     _require_table(w_gate, "w_gate", n_experts, x)
     _require_table(w_up, "w_up", n_experts, x)
     h = torch.empty(n_rows, dim_ffn, dtype=x.dtype, device=x.device)
+    ws, ws_bytes = _workspace(x, dim, dim_ffn, block_m, down=False, balance=balance)
     _check(
         loader.library().astrai_moe_gemm_gate_up_gather(
             x.data_ptr(), sorted_token.data_ptr(), n_tokens, tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
-            w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, block_m, h.data_ptr(), _stream(x)),
+            w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, block_m, h.data_ptr(), _ptr(ws), ws_bytes,
+            _stream(x)),
         "moe_gemm_gate_up_gather",
     )
     return h
 
 
-def _split_workspace(h: torch.Tensor, dim: int, block_m: int) -> tuple[torch.Tensor | None, int]:
-    """The down GEMMs' split-tail workspace (fp32 partial sums; see
-    ``astrai_moe_gemm_down``), allocated only where the 256-row matrix-core
-    kernel runs: (tensor or None, bytes)."""
-    if block_m != 256 or h.dtype != torch.bfloat16 or not matrix_core_supported(dim, h.shape[1], h.dtype):
-        return None, 0
-    nbytes = int(loader.library().astrai_moe_gemm_split_bytes())
-    return torch.empty(nbytes // 4, dtype=torch.float32, device=h.device), nbytes
-
-
 def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, sorted_w: torch.Tensor | None,
                   n_experts: int, dim: int, block_m: int, out: torch.Tensor | None = None,
-                  packed: bool = False, split_tail: bool = True) -> torch.Tensor:
+                  packed: bool = False, balance: bool = True) -> torch.Tensor:
     """y = down(h) * routing weight over every expert's rows (mlp.py:24, :97).
 
     ``sorted_w`` None: no routing weight (a dense expert, mlp.py:24 alone).
     ``packed``: ``w_down`` is a table of packed copies (``moe_pack_down``).
-    ``split_tail``: the 256-row kernel may split the tiles left after its last
-    whole round of compute units along K (``astrai_moe_gemm_down``); False
-    keeps every tile's single K order, whose bits do not depend on the
-    device's compute-unit count."""
+    ``balance``: the 256-row kernel may hand out the last tenth of its tiles
+    at run time and split the tiles left after its last whole round of compute
+    units along K (``astrai_moe_gemm_down``); False deals every tile in
+    advance and keeps each tile's single K order, whose bits do not depend on
+    the device's compute-unit count."""
     fn = _kernel("moe_gemm_down")
     _require_gpu(h, "h", 2)
     code = _dtype_code(h, "h")
@@ -333,7 +344,7 @@ def moe_gemm_down(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tensor, so
     _check_tiles(tiles, block_m, h, "moe_gemm_down")
     _require_table(w_down, "w_down", n_experts, h)
     y = _out_buffer(out, n_rows, dim, h)
-    ws, ws_bytes = _split_workspace(h, dim, block_m) if split_tail else (None, 0)
+    ws, ws_bytes = _workspace(h, dim, dim_ffn, block_m, down=True, balance=balance)
     if packed:
         _check(
             loader.library().astrai_moe_gemm_down_packed(
@@ -512,9 +523,10 @@ def moe_gemm_gate_up_train(x_perm: torch.Tensor, tiles: torch.Tensor, w_gate: to
     _require_table(w_up, "w_up", n_experts, x_perm)
     h = torch.empty(n_rows, dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
     gu = torch.empty(n_rows, 2 * dim_ffn, dtype=x_perm.dtype, device=x_perm.device)
+    ws, ws_bytes = _workspace(x_perm, dim, dim_ffn, bm, down=False)
     _lib_call("astrai_moe_gemm_gate_up_train", x_perm.data_ptr(), tiles.data_ptr(), tiles.numel(), w_gate.data_ptr(),
-              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, bm, h.data_ptr(), gu.data_ptr(),
-              _stream(x_perm))
+              w_up.data_ptr(), code, n_rows, n_experts, dim, dim_ffn, bm, h.data_ptr(), gu.data_ptr(), _ptr(ws),
+              ws_bytes, _stream(x_perm))
     return h, gu
 
 
@@ -546,7 +558,7 @@ def moe_gemm_down_train(h: torch.Tensor, tiles: torch.Tensor, w_down: torch.Tens
     _check_tiles(tiles, bm, h, "moe_gemm_down_train")
     _require_table(w_down, "w_down", n_experts, h)
     y, y_unw = (torch.empty(n_rows, dim, dtype=h.dtype, device=h.device) for _ in range(2))
-    ws, ws_bytes = _split_workspace(h, dim, bm)
+    ws, ws_bytes = _workspace(h, dim, dim_ffn, bm, down=True)
     _lib_call("astrai_moe_gemm_down_train", h.data_ptr(), tiles.data_ptr(), tiles.numel(), w_down.data_ptr(),
               sorted_w.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, bm, y.data_ptr(),
               y_unw.data_ptr(), _ptr(ws), ws_bytes, _stream(h))

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 6
+#define ASTRAI_MOE_ABI_VERSION 7
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -178,6 +178,15 @@ int astrai_moe_dense_tiles(int64_t n_rows, int block_m, int32_t* tiles,
  *   tiles   tile list from astrai_moe_permute (same block_m)
  *   w_gate, w_up  device arrays of n_experts pointers, each [dim_ffn, dim]
  *   h       [n_rows, dim_ffn]       dtype
+ *   workspace  scratch of the 256-row kernel, or NULL (contents need not be
+ *              initialised; calls sharing one must not overlap). With
+ *              workspace_bytes >= astrai_moe_gemm_workspace_bytes(0) the
+ *              last tenth of the work is handed out at run time from a
+ *              counter in it, so that compute units running at a higher
+ *              clock take more (the XCDs of one MI355X hold clocks several
+ *              per cent apart under load); with NULL every workgroup's tiles
+ *              are dealt in advance. Results do not depend on it (each tile
+ *              is computed the same way by whichever workgroup takes it).
  *
  * Kernels (both GEMMs): bf16 runs on the matrix cores with block_m 32, 64,
  * 128 or 256 when K is a multiple of 64 and the output columns a multiple of
@@ -192,7 +201,8 @@ int astrai_moe_gemm_gate_up(const void* x_perm, const int32_t* tiles,
                             int64_t tiles_len, const void* const* w_gate,
                             const void* const* w_up, int dtype, int64_t n_rows,
                             int n_experts, int64_t dim, int64_t dim_ffn,
-                            int block_m, void* h, void* stream);
+                            int block_m, void* h, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 /*
  * astrai_moe_gemm_gate_up reading the activation rows straight from x: row r
@@ -210,7 +220,8 @@ int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token,
                                    const void* const* w_up, int dtype,
                                    int64_t n_rows, int n_experts, int64_t dim,
                                    int64_t dim_ffn, int block_m, void* h,
-                                   void* stream);
+                                   void* workspace,
+                                   int64_t workspace_bytes, void* stream);
 
 /*
  * Grouped down projection with the routing-weight multiply fused.
@@ -222,16 +233,16 @@ int astrai_moe_gemm_gate_up_gather(const void* x, const int32_t* sorted_token,
  *   sorted_w  [n_rows]            dtype, from astrai_moe_permute; NULL for
  *                                 weight 1 (a dense expert: mlp.py:22-25)
  *   y         [n_rows, dim]       dtype
- *   workspace  fp32 partial sums for the 256-row kernel's last round, or
- *              NULL; with workspace_bytes >= astrai_moe_gemm_split_bytes()
- *              the tiles left over after the last whole round of compute
- *              units (at most half a round) are split along K over all of
- *              them and summed in a second launch, instead of holding a few
- *              units for a full tile time while the rest idle. Those tiles'
- *              fp32 sums then group K differently (within the GEMM tolerance
- *              of the whole-tile order; deterministic). Not read by other
- *              tile heights, fp32 or the general kernel. Calls that share a
- *              workspace must not overlap.
+ *   workspace  as for astrai_moe_gemm_gate_up, plus the fp32 partial sums of
+ *              the down GEMM's last round: with workspace_bytes >=
+ *              astrai_moe_gemm_workspace_bytes(1) the tiles left over after
+ *              the last whole round of compute units (at most half a round)
+ *              are split along K over all of them and summed in a second
+ *              launch, instead of holding a few units for a full tile time
+ *              while the rest idle. Those tiles' fp32 sums then group K
+ *              differently (within the GEMM tolerance of the whole-tile
+ *              order; deterministic for one compute-unit count). Not read by
+ *              other tile heights, fp32 or the general kernel.
  */
 int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                          int64_t tiles_len, const void* const* w_down,
@@ -241,12 +252,14 @@ int astrai_moe_gemm_down(const void* h, const int32_t* tiles,
                          int64_t workspace_bytes, void* stream);
 
 /*
- * Bytes of the workspace with which astrai_moe_gemm_down (and its packed and
- * training variants) may split the last round's tiles on the current device:
- * one 256 x 256 fp32 tile per compute unit (64 MiB on 256 compute units). No
- * counterpart in the reference (mlp.py:96-98 runs one F.linear per expert).
+ * Bytes of the GEMM workspace on the current device: 64 KiB of scheduling
+ * state (the run-time claim counter and a mailbox per workgroup), plus, for
+ * the down GEMMs (down != 0), one 256 x 256 fp32 tile of partial sums per
+ * compute unit (64 MiB on 256 compute units). The same sizes serve the
+ * packed and training variants. No counterpart in the reference
+ * (mlp.py:96-98 runs one F.linear per expert).
  */
-int64_t astrai_moe_gemm_split_bytes(void);
+int64_t astrai_moe_gemm_workspace_bytes(int down);
 
 /*
  * Packed expert weights (bf16). No counterpart in the reference: a cached
@@ -289,7 +302,8 @@ int astrai_moe_gemm_gate_up_packed(const void* x_perm, const int32_t* tiles,
                                    int64_t tiles_len, const void* const* w_packed,
                                    int dtype, int64_t n_rows, int n_experts,
                                    int64_t dim, int64_t dim_ffn, int block_m,
-                                   void* h, void* stream);
+                                   void* h, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
 int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles,
                                 int64_t tiles_len, const void* const* w_packed,
                                 const void* sorted_w, int dtype, int64_t n_rows,
@@ -349,7 +363,8 @@ int astrai_moe_gemm_gate_up_train(const void* x_perm, const int32_t* tiles,
                                   const void* const* w_up, int dtype,
                                   int64_t n_rows, int n_experts, int64_t dim,
                                   int64_t dim_ffn, int block_m, void* h,
-                                  void* gu, void* stream);
+                                  void* gu, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
 int astrai_moe_gemm_down_train(const void* h, const int32_t* tiles,
                                int64_t tiles_len, const void* const* w_down,
                                const void* sorted_w, int dtype, int64_t n_rows,

@@ -204,13 +204,20 @@ def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
     (6144, 8, 2, 2048, 1408, False),  # ~52 x 8: 22 K steps per tile, split 2 ways (or not, with a long tail)
     (16384, 1, 1, 512, 4096, False),  # one expert: 64 row tiles x 2 = 128 tiles, a partial first round
     (4096, 4, 2, 256, 1024, False),  # 32 row tiles x 1 column tile
+    # 48 K steps or more per tile: the last tenth of the items claimed at run time
+    (16384, 8, 2, 3072, 1024, False),  # gate/up: ~132 row tiles x 8 column tiles
+    (16384, 8, 2, 3072, 1024, True),
+    (24576, 8, 2, 1024, 4096, False),  # down: ~196 x 4, with a split tail
+    (24576, 16, 2, 512, 2048, False),  # ~200 x 2 down / x 16 gate/up, 32 steps: every tile dealt in advance
 ])
-def test_down_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
-    """The down GEMM with the last round's tiles split along K (partial sums
-    reduced in slice order) against the same GEMM with every tile whole and
-    against torch at the reference's rounding points: tiles outside the split
-    tail bit-identical, the tail within the GEMM tolerance, and the train
-    variant's weighted output bit-identical to the inference one."""
+def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
+    """The 256-row GEMMs with their workspace (the last tenth of the tiles
+    claimed at run time; the down GEMM's last round split along K, partial
+    sums reduced in slice order) against the same GEMMs with every tile dealt
+    in advance and run whole, and against torch at the reference's rounding
+    points: gate/up bit-identical, down tiles outside the split tail
+    bit-identical and the tail within the GEMM tolerance, and the train
+    variants' outputs bit-identical to the inference ones."""
     dtype = torch.bfloat16
     route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=11)
     g = torch.Generator(device=gpu).manual_seed(4)
@@ -222,11 +229,18 @@ def test_down_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
     tu = ops.expert_weight_table([e.up for e in experts], (dim_ffn, dim))
     td = ops.expert_weight_table([e.down for e in experts], (dim, dim_ffn))
     h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    h_static = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm, balance=False)
+    h_gather = ops.moe_gemm_gate_up_gather(x, perm.sorted_token, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
     if packed:
+        tpg = ops.expert_weight_table([ops.moe_pack_gate_up(e.gate, e.up) for e in experts], (2 * dim_ffn, dim))
+        h_packed = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tpg, tpg, n_exp, dim_ffn, bm, packed=True)
         td = ops.expert_weight_table([ops.moe_pack_down(e.down) for e in experts], (dim, dim_ffn))
     y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed)
-    y_whole = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed, split_tail=False)
+    y_whole = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed, balance=False)
     torch.cuda.synchronize()
+    assert torch.equal(h, h_static) and torch.equal(h, h_gather)
+    if packed:
+        assert torch.equal(h, h_packed)
     tl = perm.tiles.cpu().tolist()
     n_live, capacity = tl[0], (len(tl) - 4) // 3
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
@@ -253,9 +267,10 @@ def test_down_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
         y_ref = F.linear(h[a:b], w.down) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
         torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
     if not packed:
+        h_tr, _ = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn)
         y_tr, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_exp, dim)
         torch.cuda.synchronize()
-        assert torch.equal(y_tr, y)
+        assert torch.equal(h_tr, h) and torch.equal(y_tr, y)
         for e, w in enumerate(experts):
             a, b = offs[e], offs[e + 1]
             if a < b:
@@ -350,80 +365,6 @@ def test_long_k_rows(gpu, n_tok, n_exp, top_k, dim, dim_ffn, block_m):
         torch.testing.assert_close(h[a:b], u * F.silu(g), **BF16_TOL)
         y_ref = F.linear(h[a:b].float(), w.down.float()).to(dtype) * perm.sorted_w[a:b].unsqueeze(-1)
         torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
-
-
-def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
-    """Tail tiles and K slices of the 256-row down kernel's last round, as the
-    kernel decides them: (L, S), S = 1 when the tail runs whole."""
-    grid = min(capacity * n_tiles_n, cus)
-    total = n_live * n_tiles_n
-    left = total % grid
-    s = min(grid // left, ksteps // 8) if 0 < left and 2 * left <= grid else 1
-    return (left, s) if s >= 2 else (0, 1)
-
-
-@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn,packed", [
-    (8192, 8, 2, 1024, 2048, False),  # ~68 row tiles x 4 column tiles: a short last round, split 4 ways
-    (8192, 8, 2, 1024, 2048, True),
-    (6144, 8, 2, 2048, 1408, False),  # ~52 x 8: 22 K steps per tile, split 2 ways (or not, with a long tail)
-    (16384, 1, 1, 512, 4096, False),  # one expert: 64 row tiles x 2 = 128 tiles, a partial first round
-    (4096, 4, 2, 256, 1024, False),  # 32 row tiles x 1 column tile
-])
-def test_down_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
-    """The down GEMM with the last round's tiles split along K (partial sums
-    reduced in slice order) against the same GEMM with every tile whole and
-    against torch at the reference's rounding points: tiles outside the split
-    tail bit-identical, the tail within the GEMM tolerance, and the train
-    variant's weighted output bit-identical to the inference one."""
-    dtype = torch.bfloat16
-    route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=11)
-    g = torch.Generator(device=gpu).manual_seed(4)
-    x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
-    experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=6)
-    bm = 256
-    perm = ops.moe_permute(route, x, n_exp, bm)
-    tg = ops.expert_weight_table([e.gate for e in experts], (dim_ffn, dim))
-    tu = ops.expert_weight_table([e.up for e in experts], (dim_ffn, dim))
-    td = ops.expert_weight_table([e.down for e in experts], (dim, dim_ffn))
-    h = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
-    if packed:
-        td = ops.expert_weight_table([ops.moe_pack_down(e.down) for e in experts], (dim, dim_ffn))
-    y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed)
-    y_whole = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed, split_tail=False)
-    torch.cuda.synchronize()
-    tl = perm.tiles.cpu().tolist()
-    n_live, capacity = tl[0], (len(tl) - 4) // 3
-    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
-    n_tiles_n = -(-dim // 256)
-    left, s = _tail_split(n_live, n_tiles_n, capacity, dim_ffn // 64, cus)
-    print(f"{n_live} row tiles x {n_tiles_n}: {left} tail tiles split {s} ways", flush=True)
-    # which (row tile, column tile) blocks differ between the split and whole orders
-    row_tile = torch.full((h.shape[0],), -1, dtype=torch.long)
-    for i in range(n_live):
-        r0, end = tl[5 + 3 * i], tl[6 + 3 * i]
-        row_tile[r0:min(r0 + bm, end)] = i
-    diff = (y != y_whole).cpu()
-    rows, cols = diff.nonzero(as_tuple=True)
-    blocks = {(int(row_tile[r]), int(c) // 256) for r, c in zip(rows.tolist(), cols.tolist())}
-    assert len(blocks) <= left, (len(blocks), left)
-    if s == 1:
-        assert torch.equal(y, y_whole)
-    torch.testing.assert_close(y, y_whole, **BF16_TOL)
-    offs = perm.expert_offsets.tolist()
-    for e, w in enumerate(experts):
-        a, b = offs[e], offs[e + 1]
-        if a == b:
-            continue
-        y_ref = F.linear(h[a:b], w.down) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
-        torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
-    if not packed:
-        y_tr, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_exp, dim)
-        torch.cuda.synchronize()
-        assert torch.equal(y_tr, y)
-        for e, w in enumerate(experts):
-            a, b = offs[e], offs[e + 1]
-            if a < b:
-                torch.testing.assert_close(y_unw[a:b], F.linear(h[a:b], w.down), **BF16_TOL)
 
 
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [

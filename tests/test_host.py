@@ -188,13 +188,23 @@ def test_abi_rejects_bad_arguments_with_message():
     # training / backward entry points: every call below is refused on the host
     # (the dummy pointers are never dereferenced); fp32 and general shapes are
     # accepted, so they do not appear here with dummy pointers
-    rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 7, 4, 2, 256, 128, 256, 1, 1, None)
+    rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 7, 4, 2, 256, 128, 256, 1, 1, None, 0, None)
     assert rc == -1 and "dtype" in loader.last_error()
-    rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 1, 4, 2, 256, 128, 32, 1, 1, None)
+    rc = lib.astrai_moe_gemm_gate_up_train(1, 1, 7, 1, 1, 1, 4, 2, 256, 128, 32, 1, 1, None, 0, None)
     assert rc == -1 and "256-row tile list" in loader.last_error()
     rc = lib.astrai_moe_gemm_down_train(1, 1, 7, 1, 1, 1, 4, 2, 0, 256, 256, 1, 1, None, 0, None)
     assert rc == -1 and "dims" in loader.last_error()
-    # the split-tail workspace of the down GEMMs: optional, aligned, size >= 0
+    # the GEMM workspace (run-time claims, split tail): optional, aligned, size >= 0
+    rc = lib.astrai_moe_gemm_gate_up(16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 16, -1, None)
+    assert rc == -1 and "negative workspace size" in loader.last_error()
+    rc = lib.astrai_moe_gemm_gate_up_gather(16, 16, 2, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 8, 1 << 16, None)
+    assert rc == -1 and "workspace must be 16-byte aligned" in loader.last_error()
+    rc = lib.astrai_moe_gemm_gate_up_packed(16, 16, 7, 16, 1, 4, 2, 256, 256, 256, 16, 8, 1 << 16, None)
+    assert rc == -1 and "workspace must be 16-byte aligned" in loader.last_error()
+    rc = lib.astrai_moe_gemm_gate_up_train(16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 16, 8, 1 << 16, None)
+    assert rc == -1 and "workspace must be 16-byte aligned" in loader.last_error()
+    assert lib.astrai_moe_gemm_workspace_bytes(0) == 1 << 16
+    assert lib.astrai_moe_gemm_workspace_bytes(1) > lib.astrai_moe_gemm_workspace_bytes(0)
     rc = lib.astrai_moe_gemm_down(16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 16, -1, None)
     assert rc == -1 and "negative workspace size" in loader.last_error()
     rc = lib.astrai_moe_gemm_down(16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 8, 1 << 20, None)
