@@ -363,6 +363,10 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
 // tiles: item i < full is logical tile i, item full + u is unit u (tile
 // full + u / S, slice u % S).
 constexpr int kSplitMinSteps = 8;
+// Tiles of fewer K steps are never split: the reduce launch and the partial
+// sums' traffic (~15 us at 16 tiles) cost about what splitting a short tile
+// saves (the fine-grained shape's 22-step down tiles take ~31 us).
+constexpr int kSplitMinTileSteps = 64;
 constexpr int kSplitUnitFloats = kMfmaBigBM * 256;  // fp32 accumulators of one 256 x 256 tile
 
 template <int GM>
@@ -966,12 +970,13 @@ int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const v
   const int64_t n_tiles_n = ceil_div(N, kGateUp ? Cfg::BN / 2 : Cfg::BN);  // the last may be partial
   int64_t grid = 0;
   if (int rc = persistent_grid(capacity, n_tiles_n, &grid)) return rc;
-  // run-time claims need the scheduling block; the down GEMMs' tail can be
-  // split when the partial sums hold a unit per workgroup
-  int32_t* sched = (ws.base != nullptr && ws.bytes >= kSchedBytes && grid <= kMaxSchedGroups)
-                       ? static_cast<int32_t*>(ws.base)
-                       : nullptr;
-  float* part = (!kGateUp && sched != nullptr &&
+  // run-time claims need the scheduling block and long tiles; the down
+  // GEMMs' tail is split when its tiles are long and the partial sums hold a
+  // unit per workgroup
+  const int64_t ksteps = K / kBK;
+  const bool have_ws = ws.base != nullptr && ws.bytes >= kSchedBytes && grid <= kMaxSchedGroups;
+  int32_t* sched = (have_ws && ksteps >= kDynamicMinSteps) ? static_cast<int32_t*>(ws.base) : nullptr;
+  float* part = (!kGateUp && have_ws && ksteps >= kSplitMinTileSteps &&
                  ws.bytes >= kSchedBytes + grid * (int64_t)sizeof(float) * kSplitUnitFloats)
                     ? reinterpret_cast<float*>(static_cast<char*>(ws.base) + kSchedBytes)
                     : nullptr;

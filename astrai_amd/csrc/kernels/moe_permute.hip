@@ -22,6 +22,10 @@
 //                   host synchronisation is needed. Splitting the column sums
 //                   off into many blocks keeps the one-block part short: it
 //                   walks n_chunks / kRangeChunks rows instead of n_chunks.
+//   For histograms of at most kFusedScanInts counts (every workload of the
+//   benchmark: up to 512 chunks over 64 experts) neither runs: each scatter
+//   workgroup reads all chunk histograms itself (fused_bases) and workgroup
+//   0 writes the offsets and the tile list, one launch instead of two.
 //   scatter_kernel  grid (chunk, column split). A chunk's first slot in each
 //                   expert's segment is its range's base plus the histograms
 //                   of the earlier chunks of its range. Wave 0 ranks the chunk's
@@ -194,14 +198,129 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   }
 }
 
-template <typename T, bool kVec>
+// Exclusive prefix sums over the block (blockDim.x == kScatterThreads) of two
+// values per thread at once (each thread holding the sums of its own run),
+// and their block totals.
+__device__ void scatter_block_exclusive_scan2(int& a, int& b, int* s_wave, int& total_a, int& total_b) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int ia = a, ib = b;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int oa = __shfl_up(ia, off, 64);
+    const int ob = __shfl_up(ib, off, 64);
+    if (lane >= off) ia += oa, ib += ob;
+  }
+  if (lane == 63) s_wave[wave] = ia, s_wave[kScatterThreads / 64 + wave] = ib;
+  __syncthreads();
+  int before_a = 0, before_b = 0;
+  total_a = total_b = 0;
+#pragma unroll
+  for (int w = 0; w < kScatterThreads / 64; ++w) {
+    const int ta = s_wave[w], tb = s_wave[kScatterThreads / 64 + w];
+    if (w < wave) before_a += ta, before_b += tb;
+    total_a += ta, total_b += tb;
+  }
+  a = before_a + ia - a;
+  b = before_b + ib - b;
+}
+
+// The scan folded into the scatter, for histograms of at most
+// kFusedScanInts counts: every workgroup reads all chunk histograms, V
+// experts per load, and forms each expert's total and its count in the
+// chunks before this one; an exclusive scan of the totals gives the expert
+// offsets, and cnt[e] = offset + earlier count is the chunk's first slot in
+// expert e's segment. Workgroup (0, 0) also writes the expert offsets and
+// the GEMM tile list (as scan_kernel does). Replaces a one-workgroup launch
+// whose fixed cost (~5 us) exceeded its work at these sizes.
+constexpr int kFusedScanInts = 32768;
+
+template <int V>
+__device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, int n_experts, int64_t chunk,
+                            int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
+                            int32_t* __restrict__ tiles, int* cnt, int* s_tot, int* s_wave) {
+  const int t = threadIdx.x;
+  const int cw = n_experts / V;  // V divides n_experts
+  const int R = cw >= kScatterThreads ? 1 : kScatterThreads / cw;
+  typedef int vint __attribute__((ext_vector_type(V)));
+  // partial column sums: thread (g, col) takes rows g, g + R, ... of its column(s)
+  if (t < R * cw || cw >= kScatterThreads) {
+    for (int col = cw >= kScatterThreads ? t : t % cw; col < cw; col += kScatterThreads) {
+      const int g = cw >= kScatterThreads ? 0 : t / cw;
+      vint tot = 0, pre = 0;
+#pragma unroll 16
+      for (int64_t c = g; c < nc; c += R) {
+        const vint h = *reinterpret_cast<const vint*>(chunk_hist + c * n_experts + col * V);
+        tot += h;
+        if (c < chunk) pre += h;
+      }
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        s_tot[g * n_experts + col * V + v] = tot[v];
+        s_tot[(R + g) * n_experts + col * V + v] = pre[v];
+      }
+      if (cw < kScatterThreads) break;
+    }
+  }
+  __syncthreads();
+  // per expert: total and earlier count; thread t holds experts 4 t .. 4 t + 3
+  int tot4[4], pre4[4], run = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * t + j;
+    tot4[j] = pre4[j] = 0;
+    if (e < n_experts)
+      for (int g = 0; g < R; ++g) tot4[j] += s_tot[g * n_experts + e], pre4[j] += s_tot[(R + g) * n_experts + e];
+    run += tot4[j];
+  }
+  const bool write_list = blockIdx.x == 0 && blockIdx.y == 0;
+  int ntile_run = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ntile_run += (tot4[j] + block_m - 1) / block_m;
+  int n_rows = 0, n_tiles = 0;
+  int off = run, tile0 = ntile_run;
+  scatter_block_exclusive_scan2(off, tile0, s_wave, n_rows, n_tiles);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * t + j;
+    if (e < n_experts) {
+      cnt[e] = off + pre4[j];
+      if (write_list) {
+        expert_offsets[e] = off;
+        const int ntile = (tot4[j] + block_m - 1) / block_m;
+        for (int k = 0; k < ntile && tile0 + k < tile_capacity; ++k) {
+          int32_t* tt = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)(tile0 + k) * ASTRAI_MOE_TILE_STRIDE;
+          tt[0] = e;
+          tt[1] = off + k * block_m;
+          tt[2] = off + tot4[j];
+        }
+        tile0 += ntile;
+      }
+      off += tot4[j];
+    }
+  }
+  if (write_list && t == 0) {
+    expert_offsets[n_experts] = n_rows;
+    tiles[0] = n_tiles;
+    tiles[1] = block_m;
+    tiles[2] = (int32_t)tile_capacity;
+    tiles[3] = 0;
+  }
+  __syncthreads();
+}
+
+// kFusedV > 0: the scan is folded in (fused_bases, kFusedV experts per
+// load); range_base and range_chunks are then unused.
+template <typename T, bool kVec, int kFusedV = 0>
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     const int32_t* __restrict__ topk_idx, const T* __restrict__ topk_w,
     const int32_t* __restrict__ chunk_hist, const int32_t* __restrict__ range_base,
     int range_chunks, const T* __restrict__ x,
     int64_t n_tokens, int n_experts, int top_k, int64_t dim,
     int32_t* __restrict__ sorted_token, T* __restrict__ sorted_w,
-    int32_t* __restrict__ token_pos, T* __restrict__ x_perm) {
+    int32_t* __restrict__ token_pos, T* __restrict__ x_perm,
+    int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ tiles) {
   __shared__ int cnt[ASTRAI_MOE_MAX_EXPERTS];
   const bool write_index = blockIdx.y == 0;
   __shared__ int pos_l[ASTRAI_MOE_CHUNK_TOKENS * ASTRAI_MOE_MAX_TOPK];
@@ -210,7 +329,12 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   const int nt = (int)min((int64_t)ASTRAI_MOE_CHUNK_TOKENS, n_tokens - t0);
   const int n_ent = nt * top_k;
   const int64_t n_rows = n_tokens * top_k;
-  {
+  if constexpr (kFusedV > 0) {
+    __shared__ int s_tot[2 * 4 * kScatterThreads];
+    __shared__ int s_wave[2 * kScatterThreads / 64];
+    fused_bases<kFusedV>(chunk_hist, (int64_t)gridDim.x, n_experts, chunk, block_m, tile_capacity, expert_offsets,
+                         tiles, cnt, s_tot, s_wave);
+  } else {
     // the chunk's first slot per expert: its range's base plus the earlier
     // chunks of the range
     const int64_t r = chunk / range_chunks;
@@ -219,8 +343,8 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
       for (int64_t c = r * range_chunks; c < chunk; ++c) b += chunk_hist[c * n_experts + e];
       cnt[e] = b;
     }
+    __syncthreads();
   }
-  __syncthreads();
 
   const int lane = threadIdx.x & 63;
   if (threadIdx.x < 64) {
@@ -334,6 +458,17 @@ int64_t permute_scratch_ints(int64_t n_tokens, int n_experts) {
   return ceil_div(n_chunks(n_tokens), scan_range_chunks(n_tokens, n_experts)) * n_experts;
 }
 
+template <typename T, bool kVec, int kFusedV>
+void launch_scatter(dim3 grid, hipStream_t s, const int32_t* topk_idx, const void* topk_w, const int32_t* chunk_hist,
+                    const int32_t* range_base, int range_chunks, const void* x, int64_t n_tokens, int n_experts,
+                    int top_k, int64_t dim, int32_t* sorted_token, void* sorted_w, int32_t* token_pos, void* x_perm,
+                    int block_m, int64_t tile_capacity, int32_t* expert_offsets, int32_t* tiles) {
+  hipLaunchKernelGGL((scatter_kernel<T, kVec, kFusedV>), grid, dim3(kScatterThreads), 0, s, topk_idx,
+                     static_cast<const T*>(topk_w), chunk_hist, range_base, range_chunks, static_cast<const T*>(x),
+                     n_tokens, n_experts, top_k, dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
+                     static_cast<T*>(x_perm), block_m, tile_capacity, expert_offsets, tiles);
+}
+
 template <typename T>
 int launch_permute(const int32_t* topk_idx, const void* topk_w,
                    const int32_t* chunk_hist, const void* x, int64_t n_tokens,
@@ -343,21 +478,25 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
                    int32_t* tiles, int64_t tile_capacity, int32_t* chunk_base,
                    hipStream_t s) {
   const int64_t nc = n_chunks(n_tokens);
-  const int range_chunks = scan_range_chunks(n_tokens, n_experts);
+  // small histograms: the scan is folded into the scatter (fused_bases)
+  const bool fused = nc > 0 && nc * n_experts <= kFusedScanInts;
+  const int range_chunks = fused ? 1 : scan_range_chunks(n_tokens, n_experts);
   const int64_t n_ranges = ceil_div(nc, range_chunks);
   int32_t* range_base = chunk_base;  // n_ranges * n_experts <= n_chunks * n_experts
   int rc = ASTRAI_MOE_OK;
-  if (range_chunks > 1) {
-    hipLaunchKernelGGL(range_sum_kernel, dim3((unsigned)n_ranges), dim3(256), 0, s,
-                       chunk_hist, nc, n_experts, range_base);
-    if ((rc = check_launch("range_sum_kernel"))) return rc;
+  if (!fused) {
+    if (range_chunks > 1) {
+      hipLaunchKernelGGL(range_sum_kernel, dim3((unsigned)n_ranges), dim3(256), 0, s,
+                         chunk_hist, nc, n_experts, range_base);
+      if ((rc = check_launch("range_sum_kernel"))) return rc;
+    }
+    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s,
+                       range_chunks > 1 ? range_base : chunk_hist, n_ranges,
+                       n_experts, block_m, tile_capacity, expert_offsets,
+                       range_base, tiles);
+    rc = check_launch("scan_kernel");
+    if (rc || nc == 0) return rc;
   }
-  hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s,
-                     range_chunks > 1 ? range_base : chunk_hist, n_ranges,
-                     n_experts, block_m, tile_capacity, expert_offsets,
-                     range_base, tiles);
-  rc = check_launch("scan_kernel");
-  if (rc || nc == 0) return rc;
   const bool vec = (dim * (int64_t)sizeof(T)) % 16 == 0 &&
                    (reinterpret_cast<uintptr_t>(x) % 16) == 0 &&
                    (reinterpret_cast<uintptr_t>(x_perm) % 16) == 0;
@@ -368,22 +507,20 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
   if (splits < 1 || x_perm == nullptr) splits = 1;
   if (splits > 65535) splits = 65535;
   const dim3 grid((unsigned)nc, (unsigned)splits);
-  if (vec)
-    hipLaunchKernelGGL((scatter_kernel<T, true>), grid,
-                       dim3(kScatterThreads), 0, s, topk_idx,
-                       static_cast<const T*>(topk_w), chunk_hist, range_base,
-                       range_chunks, static_cast<const T*>(x), n_tokens,
-                       n_experts, top_k,
-                       dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
-                       static_cast<T*>(x_perm));
-  else
-    hipLaunchKernelGGL((scatter_kernel<T, false>), grid,
-                       dim3(kScatterThreads), 0, s, topk_idx,
-                       static_cast<const T*>(topk_w), chunk_hist, range_base,
-                       range_chunks, static_cast<const T*>(x), n_tokens,
-                       n_experts, top_k,
-                       dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
-                       static_cast<T*>(x_perm));
+  // the fused scan reads 16-byte vectors of 4 experts where rows allow it
+  const bool v4 = n_experts % 4 == 0 && reinterpret_cast<uintptr_t>(chunk_hist) % 16 == 0;
+#define ASTRAI_SCATTER(VEC, FV)                                                                                       \
+  launch_scatter<T, VEC, FV>(grid, s, topk_idx, topk_w, chunk_hist, range_base, range_chunks, x, n_tokens, n_experts, \
+                             top_k, dim, sorted_token, sorted_w, token_pos, x_perm, block_m, tile_capacity,          \
+                             expert_offsets, tiles)
+  if (!fused) {
+    if (vec) ASTRAI_SCATTER(true, 0); else ASTRAI_SCATTER(false, 0);
+  } else if (v4) {
+    if (vec) ASTRAI_SCATTER(true, 4); else ASTRAI_SCATTER(false, 4);
+  } else {
+    if (vec) ASTRAI_SCATTER(true, 1); else ASTRAI_SCATTER(false, 1);
+  }
+#undef ASTRAI_SCATTER
   return check_launch("scatter_kernel");
 }
 

@@ -190,7 +190,10 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
 
 def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
     """Tail tiles and K slices of the 256-row down kernel's last round, as the
-    kernel decides them: (L, S), S = 1 when the tail runs whole."""
+    kernel decides them: (L, S), S = 1 when the tail runs whole (tiles of
+    fewer than 64 K steps never split)."""
+    if ksteps < 64:
+        return 0, 1
     grid = min(capacity * n_tiles_n, cus)
     total = n_live * n_tiles_n
     left = total % grid
@@ -199,9 +202,9 @@ def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
 
 
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn,packed", [
-    (8192, 8, 2, 1024, 2048, False),  # ~68 row tiles x 4 column tiles: a short last round, split 4 ways
-    (8192, 8, 2, 1024, 2048, True),
-    (6144, 8, 2, 2048, 1408, False),  # ~52 x 8: 22 K steps per tile, split 2 ways (or not, with a long tail)
+    (8192, 8, 2, 1024, 4096, False),  # ~68 row tiles x 4 column tiles: a short last round, split 8 ways
+    (8192, 8, 2, 1024, 4096, True),
+    (6144, 8, 2, 2048, 1408, False),  # ~52 x 8: 22 K steps per tile, too short to split
     (16384, 1, 1, 512, 4096, False),  # one expert: 64 row tiles x 2 = 128 tiles, a partial first round
     (4096, 4, 2, 256, 1024, False),  # 32 row tiles x 1 column tile
     # 48 K steps or more per tile: the last tenth of the items claimed at run time
