@@ -88,6 +88,15 @@ __device__ inline void lds_barrier() {
 // The persistent tile walk. Round r takes logical tile r * G + slot, where
 // slot gives the workgroups of one XCD a contiguous range of logical tiles;
 // logical tiles walk GM row tiles for every column tile.
+//
+// GM = 16 walks a group of 16 row tiles as two halves of 8 side by side: for
+// each run of 4 column tiles, the first half's 8 x 4 block, then the second
+// half's. With 32 workgroups per XCD, neighbouring XCDs then take the two
+// halves of the same 4 column tiles at the same time, so each weight tile of
+// an expert whose rows fill the group leaves HBM once (the second XCD finds
+// it in the Infinity Cache) where two groups of 8 walked one after the other
+// read it twice, while every XCD keeps its 8 x 4 block of tiles (12 operand
+// strips per 32 tiles through its L2).
 template <int GM>
 struct TileWalk {
   int G, n_live, total, group_size;
@@ -110,8 +119,24 @@ struct TileWalk {
     const int first_m = (logical / group_size) * GM;
     const int gm = min(GM, n_live - first_m);
     const int in_group = logical - (first_m / GM) * group_size;
-    mt = first_m + in_group % gm;
-    nt = in_group / gm;
+    if constexpr (GM == 16) {
+      // runs of 4 column tiles, each the first half's block then the second's
+      const int ga = min(8, gm), gb = gm - ga;
+      const int n_tiles_n = group_size / GM;
+      const int c = min(in_group / (gm * 4), (n_tiles_n - 1) / 4);
+      const int j = in_group - c * gm * 4;
+      const int wc = min(4, n_tiles_n - 4 * c);
+      if (j < ga * wc) {
+        mt = first_m + j % ga;
+        nt = 4 * c + j / ga;
+      } else {
+        mt = first_m + ga + (j - ga * wc) % gb;
+        nt = 4 * c + (j - ga * wc) / gb;
+      }
+    } else {
+      mt = first_m + in_group % gm;
+      nt = in_group / gm;
+    }
   }
   // this workgroup's tile at `logical` (>= total: none)
   __device__ int seek(int logical, int& mt, int& nt) const {

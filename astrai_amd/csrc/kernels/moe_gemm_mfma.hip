@@ -251,7 +251,13 @@ __host__ __device__ constexpr int staged_row_bytes() {
 // ===========================================================================
 template <bool kGateUp>
 struct StreamCfg {
-  static constexpr int BM = 256, BN = 256, GM = 8;
+  // row tiles per group of the walk: gate/up walks 8 row tiles for every
+  // column tile (each round's 8 activation strips are read by all 8 XCDs);
+  // down walks paired halves of 8 (TileWalk, GM = 16). Measured in one
+  // process, builds alternating, on two boxes: the paired walk took the down
+  // GEMMs +0.1 / +0.5 % (Mixtral shape) and +1.1 / +4.8 % (fine-grained),
+  // gate/up -2.7 % and -8.7 % (its activation strips then serve 4 XCDs).
+  static constexpr int BM = 256, BN = 256, GM = kGateUp ? 8 : 16;
   static constexpr int WGM = 2, WGN = 4, MW = 8, DW = 4;  // matrix-core waves (WGM x WGN), DMA waves
   static constexpr int WAVES = MW + DW, THREADS = WAVES * 64;
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // 128 x 64 per matrix-core wave
