@@ -263,14 +263,30 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
     }
   }
   __syncthreads();
+  // fold the R partial rows into row 0 as a tree (few experts leave R up to
+  // 256: summed by one thread per expert, the rows took ~15 us)
+  if (R > 1) {
+    int half = 1;
+    while (2 * half < R) half *= 2;
+    const int g = t / cw, col = t % cw;
+    for (int live = R; half > 0; live = half, half /= 2) {
+      if (g < half && g + half < live) {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          s_tot[g * n_experts + col * V + v] += s_tot[(g + half) * n_experts + col * V + v];
+          s_tot[(R + g) * n_experts + col * V + v] += s_tot[(R + g + half) * n_experts + col * V + v];
+        }
+      }
+      __syncthreads();
+    }
+  }
   // per expert: total and earlier count; thread t holds experts 4 t .. 4 t + 3
   int tot4[4], pre4[4], run = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = 4 * t + j;
     tot4[j] = pre4[j] = 0;
-    if (e < n_experts)
-      for (int g = 0; g < R; ++g) tot4[j] += s_tot[g * n_experts + e], pre4[j] += s_tot[(R + g) * n_experts + e];
+    if (e < n_experts) tot4[j] = s_tot[e], pre4[j] = s_tot[R * n_experts + e];
     run += tot4[j];
   }
   const bool write_list = blockIdx.x == 0 && blockIdx.y == 0;
@@ -329,6 +345,21 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   const int nt = (int)min((int64_t)ASTRAI_MOE_CHUNK_TOKENS, n_tokens - t0);
   const int n_ent = nt * top_k;
   const int64_t n_rows = n_tokens * top_k;
+  // The chunk's routing entries are loaded first, so that their latency
+  // overlaps that of the expert bases below; they reach LDS afterwards.
+  constexpr int kEnt = ASTRAI_MOE_CHUNK_TOKENS * ASTRAI_MOE_MAX_TOPK;
+  constexpr int kEntPerThread = kEnt / kScatterThreads;
+  static_assert(kEnt % kScatterThreads == 0, "entries per thread");
+  __shared__ int s_e[kEnt];
+  __shared__ T s_w[kEnt];
+  int pe[kEntPerThread];
+  T pw[kEntPerThread];
+#pragma unroll
+  for (int j = 0; j < kEntPerThread; ++j) {
+    const int i = threadIdx.x + j * kScatterThreads;
+    pe[j] = i < n_ent ? topk_idx[t0 * top_k + i] : -1;
+    pw[j] = (i < n_ent && write_index) ? topk_w[t0 * top_k + i] : T(0);
+  }
   if constexpr (kFusedV > 0) {
     __shared__ int s_tot[2 * 4 * kScatterThreads];
     __shared__ int s_wave[2 * kScatterThreads / 64];
@@ -345,6 +376,12 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     }
     __syncthreads();
   }
+#pragma unroll
+  for (int j = 0; j < kEntPerThread; ++j) {
+    const int i = threadIdx.x + j * kScatterThreads;
+    if (i < n_ent) s_e[i] = pe[j], s_w[i] = pw[j];
+  }
+  __syncthreads();
 
   const int lane = threadIdx.x & 63;
   if (threadIdx.x < 64) {
@@ -353,7 +390,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int base = 0; base < n_ent; base += 64) {
       const int i = base + lane;
-      int e = i < n_ent ? topk_idx[t0 * top_k + i] : -1;
+      int e = i < n_ent ? s_e[i] : -1;
       const bool valid = e >= 0 && e < n_experts;
       uint64_t peers = __ballot(valid);
       for (int b = 0; b < nbits; ++b) {
@@ -374,7 +411,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
           token_pos[t0 * top_k + i] = ok ? p : -1;
           if (ok) {
             sorted_token[p] = (int32_t)(t0 + i / top_k);
-            sorted_w[p] = topk_w[t0 * top_k + i];
+            sorted_w[p] = s_w[i];
           }
         }
       }
