@@ -49,12 +49,12 @@ PEAK_HBM_GBS = 8000.0
 # counts this part's 128-byte read requests as 64 bytes), hence the 2. Sources:
 # profiles/moe_layer_*.md of each workload.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
-    "moe_bf16_d4096_f14336_e8_k2_t16384": (6155726.1 * 2 + 917505.3) * 1024,
-    "moe_bf16_d2048_f1408_e64_k6_t8192": (779643.7 * 2 + 135168.2) * 1024,
-    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (760612.6 * 2 + 135168.1) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t64": (1567671.9 * 2 + 1538.2) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t1024": (1681513.7 * 2 + 24587.2) * 1024,
-    "moe_fp32_d512_f1024_e8_k2_t1024": (70495.9 * 2 + 8193.0) * 1024,
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (6163566.0 * 2 + 917612.9) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192": (779667.6 * 2 + 135168.0) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (760961.2 * 2 + 135168.1) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t64": (1567802.7 * 2 + 1538.2) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t1024": (1685293.1 * 2 + 24585.0) * 1024,
+    "moe_fp32_d512_f1024_e8_k2_t1024": (70498.3 * 2 + 8193.9) * 1024,
 }
 
 
