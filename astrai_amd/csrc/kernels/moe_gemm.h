@@ -127,10 +127,13 @@ int launch_row_grad(const void* dout, const int32_t* sorted_token,
 int launch_dgrad_down(const void* dy, const int32_t* tiles, int64_t capacity,
                       const void* const* w_down, const void* gu, int64_t dim,
                       int64_t dim_ffn, void* dg, void* du, hipStream_t s);
-// dx [rows, n] = bf16(d . W[e]) (+ add, rounded again), W[e] [k, n];
+// dx [rows, n] = bf16(d . W[e]) (+ add, rounded again), W[e] [k, n]; ws as
+// the down GEMM's (gemm_workspace_bytes(true)): the last round's tiles split
+// along K;
 int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity,
                     const void* const* w, int64_t k, int64_t n,
-                    const void* add, void* dx, hipStream_t s);
+                    const void* add, void* dx, hipStream_t s,
+                    const GemmWorkspace& ws = {});
 // dw[e] [m, n] = a[rows_e]^T . b[rows_e] for every expert with rows
 // (a: [rows, m], b: [rows, n]); experts without rows are not written.
 int launch_wgrad(const void* a, const void* b, const int32_t* offsets,

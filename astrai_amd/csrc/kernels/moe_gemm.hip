@@ -467,11 +467,13 @@ extern "C" int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles, 
 extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, const int32_t* tiles, int64_t tiles_len,
                                              const void* const* w_gate, const void* const* w_up, int dtype,
                                              int64_t n_rows, int n_experts, int64_t dim_ffn, int64_t dim,
-                                             int block_m, void* dx_perm, void* stream) {
+                                             int block_m, void* dx_perm, void* workspace, int64_t workspace_bytes,
+                                             void* stream) {
   clear_error();
   int rc = check_common("gemm_dgrad_gate_up", dg, tiles, tiles_len, dtype, n_rows, n_experts, dim_ffn, dim, block_m,
                         dx_perm);
   if (rc) return rc;
+  if ((rc = check_workspace("gemm_dgrad_gate_up", workspace, workspace_bytes))) return rc;
   if ((rc = check_train("gemm_dgrad_gate_up", dtype, dim, dim_ffn, block_m))) return rc;
   if (n_rows == 0) return ASTRAI_MOE_OK;
   ASTRAI_REQUIRE(du && w_gate && w_up, "gemm_dgrad_gate_up: null weight table or buffer");
@@ -481,8 +483,9 @@ extern "C" int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du, con
   if (mfma_train_shape(dtype, dim, dim_ffn)) {
     ASTRAI_REQUIRE(aligned16_ptr(dg) && aligned16_ptr(du) && aligned16_ptr(dx_perm),
                    "gemm_dgrad_gate_up: buffers must be 16-byte aligned");
-    if ((rc = launch_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;
-    return launch_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s);
+    const GemmWorkspace ws{workspace, workspace_bytes};
+    if ((rc = launch_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s, ws))) return rc;
+    return launch_dgrad_in(du, tiles, capacity, w_up, dim_ffn, dim, dx_perm, dx_perm, s, ws);
   }
   if (dtype == ASTRAI_MOE_F32 && mfma_f32_bwd_supported(dim_ffn, dim, block_m, dg, dx_perm, du, nullptr)) {
     if ((rc = launch_mfma_f32_dgrad_in(dg, tiles, capacity, w_gate, dim_ffn, dim, nullptr, dx_perm, s))) return rc;

@@ -70,6 +70,8 @@ struct BwdArgs {
   int n_tiles_m, n_tiles_n;  // column tiles (dgrad), M / N tiles (wgrad)
   int capacity;              // dgrad: tile-list capacity
   int n_experts;             // wgrad
+  float* part;               // dgrad: partial sums of the split last round (null: the tail runs whole)
+  int grid;                  // workgroups of the GEMM launch (the split reduce recomputes its walk)
 };
 
 struct BwdCfg {
@@ -90,27 +92,55 @@ struct BwdCfg {
   static_assert(16 % AR == 0 && 8 % RG == 0 && PD >= RG && PD + RG <= AR, "ring slots of a pair and its prefetch");
 };
 
+// A work item: tile (mt, nt) of expert e, K steps [k0, ksteps); unit >= 0:
+// a slice of a split tail tile whose fp32 accumulators go to part[unit].
 struct TileInfo {
-  int e, mt, nt, row0, rows, ksteps;
+  int e, mt, nt, row0, rows, k0, ksteps, unit;
 };
 
 // dgrad: the forward's tile walk over (row tile, column tile), K fixed.
+// kSplit (dgrad_in): with a partial-sum buffer the last round's tiles are
+// split along K as in the forward down GEMM (SplitWalk). The GEMM launch then
+// walks the whole tiles (items [0, full)) and a second launch of the same
+// grid the split slices (items [full, items()), at most one per workgroup),
+// so that neither kernel carries both epilogues (the branch between them
+// spilled the SwiGLU-backward epilogue's registers). dgrad_down keeps the
+// plain walk: at the register limit already, the split walk's state cost it
+// 2.5 % (same-process A/B) where its split tail gained 1 %.
+template <bool kSplit>
 struct RowTileWalk {
-  TileWalk<BwdCfg::GM> w;
+  static constexpr bool kSplitK = kSplit;  // items may start past K step 0
+  std::conditional_t<kSplit, SplitWalk<BwdCfg::GM>, TileWalk<BwdCfg::GM>> w;
   const int32_t* tiles;
-  int ksteps;
-  int G, total;
-  __device__ explicit RowTileWalk(const BwdArgs& p)
-      : w(p.tiles, p.capacity, p.n_tiles_n), tiles(p.tiles), ksteps(p.K / kBK), G(w.G), total(w.total) {}
-  __device__ int first_slot() const { return w.first_slot(); }
+  int ksteps, G, begin, total;
+  __device__ RowTileWalk(const BwdArgs& p, bool tail) : w(make_walk(p)), tiles(p.tiles), ksteps(p.K / kBK), G(w.G) {
+    if constexpr (kSplit) {
+      begin = tail ? w.full : 0;
+      total = tail ? w.items() : w.full;
+    } else {
+      begin = 0;
+      total = w.total;
+    }
+  }
+  __device__ static decltype(w) make_walk(const BwdArgs& p) {
+    if constexpr (kSplit)
+      return SplitWalk<BwdCfg::GM>(p.tiles, p.capacity, p.n_tiles_n, p.K / kBK, p.part != nullptr, p.grid);
+    else
+      return TileWalk<BwdCfg::GM>(p.tiles, p.capacity, p.n_tiles_n);
+  }
+  __device__ int first_slot() const { return begin + w.first_slot(); }
   __device__ int seek(int logical, TileInfo& t) const {
-    logical = w.seek(logical, t.mt, t.nt);
     if (logical < total) {
+      if constexpr (kSplit) {
+        w.item(logical, t.mt, t.nt, t.k0, t.ksteps, t.unit);
+      } else {
+        w.decode(logical, t.mt, t.nt);
+        t.k0 = 0, t.ksteps = ksteps, t.unit = -1;
+      }
       const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)uniform(t.mt) * ASTRAI_MOE_TILE_STRIDE;
       t.e = load_scalar(ti);
       t.row0 = load_scalar(ti + 1);
       t.rows = min(BwdCfg::BM, load_scalar(ti + 2) - t.row0);
-      t.ksteps = ksteps;
     }
     return logical;
   }
@@ -119,9 +149,10 @@ struct RowTileWalk {
 // wgrad: (expert, M tile, N tile), GM M tiles walked per N tile; experts
 // without rows are skipped; K = the expert's rows in steps of 64.
 struct ExpertWalk {
+  static constexpr bool kSplitK = false;
   const int32_t* off;
   int MT, NT, per_e, G, total;
-  __device__ explicit ExpertWalk(const BwdArgs& p)
+  __device__ ExpertWalk(const BwdArgs& p, bool)
       : off(p.offsets), MT(p.n_tiles_m), NT(p.n_tiles_n), per_e(p.n_tiles_m * p.n_tiles_n), G((int)gridDim.x),
         total(p.n_experts * p.n_tiles_m * p.n_tiles_n) {}
   __device__ int first_slot() const {
@@ -138,7 +169,9 @@ struct ExpertWalk {
     t.nt = in_group / gm;
     t.row0 = load_scalar(off + t.e);
     t.rows = load_scalar(off + t.e + 1) - t.row0;
+    t.k0 = 0;
     t.ksteps = (t.rows + kBK - 1) / kBK;
+    t.unit = -1;
     return t.rows > 0;
   }
   __device__ int seek(int logical, TileInfo& t) const {
@@ -255,15 +288,14 @@ struct BwdCursor {
   TileInfo t;
   BwdSrc<kMode> src;
   __device__ void start(const BwdArgs& p, int logical_, const TileInfo& t_, int lane) {
-    logical = logical_, t = t_, kt = 0, live = true;
+    logical = logical_, t = t_, kt = Walk::kSplitK ? t.k0 : 0, live = true;
     src.setup(p, t, lane);
   }
   __device__ void advance(const BwdArgs& p, const Walk& walk, int lane) {
     if (++kt == t.ksteps) {
-      kt = 0;
       logical = walk.seek(logical + walk.G, t);
       live = logical < walk.total;
-      if (live) src.setup(p, t, lane);
+      if (live) kt = Walk::kSplitK ? t.k0 : 0, src.setup(p, t, lane);
     }
   }
 };
@@ -420,13 +452,62 @@ __device__ __forceinline__ void bwd_epilogue_pf(f32x4_t (&acc)[BwdCfg::WM / 16][
   }
 }
 
-template <Bwd kMode, typename Cfg = BwdCfg>
+template <Bwd kMode>
+__device__ __forceinline__ void bwd_epilogue_any(f32x4_t (&acc)[BwdCfg::WM / 16][BwdCfg::WN / 16], const BwdArgs& p,
+                                                 const TileInfo& t, int wm, int wn) {
+  // input rings two (gu, 32 bytes per lane and column pair) and four row
+  // blocks deep: deeper rings spilled
+  if constexpr (kMode == Bwd::kDgradDown)
+    bwd_epilogue_pf<kMode, 2>(acc, p, t, wm, wn);
+  else if constexpr (kMode == Bwd::kDgradInAdd)
+    bwd_epilogue_pf<kMode, 4>(acc, p, t, wm, wn);
+  else
+    bwd_epilogue<kMode>(acc, p, t, wm, wn);
+}
+
+// The epilogue of a dgrad GEMM's split tail tiles: workgroup u sums the S
+// partials of tail tile u in slice order (wave w those of matrix-core wave w)
+// and runs the tile's epilogue. The walk is recomputed from the same tile
+// list and the GEMM launch's grid, so both kernels agree on the split.
+template <Bwd kMode>
+__global__ __launch_bounds__(512) void bwd_split_reduce_kernel(const BwdArgs p) {
+  static_assert(kMode == Bwd::kDgradIn || kMode == Bwd::kDgradInAdd, "only dgrad_in splits its tail");
+  const RowTileWalk<true> walk(p, true);
+  const int u = blockIdx.x;
+  if (walk.w.S < 2 || u >= walk.w.total - walk.w.full) return;
+  TileInfo t;
+  walk.seek(walk.w.full + u * walk.w.S, t);  // the tile's first slice
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16;
+  constexpr int kUnitVecs = kSplitUnitFloats / 4;
+  const f32x4_t* pp = reinterpret_cast<const f32x4_t*>(p.part) + (int64_t)u * walk.w.S * kUnitVecs +
+                      wave * (MT16 * NT16 * 64) + lane;
+  f32x4_t acc[MT16][NT16];
+#pragma unroll
+  for (int i = 0; i < MT16; ++i)
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) acc[i][j] = pp[(i * NT16 + j) * 64];
+  for (int sl = 1; sl < walk.w.S; ++sl) {
+    const f32x4_t* ps = pp + (int64_t)sl * kUnitVecs;
+#pragma unroll
+    for (int i = 0; i < MT16; ++i)
+#pragma unroll
+      for (int j = 0; j < NT16; ++j) acc[i][j] += ps[(i * NT16 + j) * 64];
+  }
+  bwd_epilogue_any<kMode>(acc, p, t, wave / BwdCfg::WGN, wave % BwdCfg::WGN);
+}
+
+// kTail: the split slices of the last round (RowTileWalk), stored as fp32
+// partial sums for bwd_split_reduce_kernel; otherwise every whole tile.
+template <Bwd kMode, bool kTail = false, typename Cfg = BwdCfg>
 __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs p) {
-  using Walk = std::conditional_t<kMode == Bwd::kWgrad, ExpertWalk, RowTileWalk>;
+  constexpr bool kSplit = kMode == Bwd::kDgradIn || kMode == Bwd::kDgradInAdd;
+  static_assert(!kTail || kSplit, "only dgrad_in splits its tail");
+  using Walk = std::conditional_t<kMode == Bwd::kWgrad, ExpertWalk, RowTileWalk<kSplit>>;
   constexpr bool kAMn = kMode == Bwd::kWgrad;  // A operand MN-major (B always is)
   __shared__ __attribute__((aligned(1024))) char smem[Cfg::LDS];
 
-  const Walk walk(p);
+  const Walk walk(p, kTail);
   TileInfo t;
   int logical = walk.seek(walk.first_slot(), t);
   if (logical >= walk.total) return;
@@ -558,14 +639,16 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs
         for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.0f;
     // every step, a tile's last included, prefetches the next step's first
     // fragments (the next tile's); one loop body, one register assignment
-    for (int kt = 0; kt < t.ksteps; ++kt) {
+    for (int kt = kSplit ? t.k0 : 0; kt < t.ksteps; ++kt) {
       step();
       rotate();
     }
     __builtin_amdgcn_sched_barrier(0);
-    // input rings two (gu, 32 bytes per lane and column pair) and four row
-    // blocks deep: deeper rings spilled
-    if constexpr (kMode == Bwd::kDgradDown)
+    // (the chain written out: through bwd_epilogue_any the compiler spilled
+    // twice as much of dgrad_down)
+    if constexpr (kTail)
+      store_partial(acc, p.part, t.unit, wave, lane);  // the reduce runs the tile's epilogue
+    else if constexpr (kMode == Bwd::kDgradDown)
       bwd_epilogue_pf<kMode, 2>(acc, p, t, wm, wn);
     else if constexpr (kMode == Bwd::kDgradInAdd)
       bwd_epilogue_pf<kMode, 4>(acc, p, t, wm, wn);
@@ -611,14 +694,33 @@ __global__ __launch_bounds__(256) void row_grad_kernel(const bf16_t* __restrict_
   if (lane == 0) dw_rows[r] = f32_to_bf16_bits(acc);
 }
 
+// ws: the dgrad_in GEMMs' workspace (null: the last round runs whole). Its
+// partial sums, one 256 KB unit per workgroup after the first kSchedBytes
+// (the forward down GEMM's layout), take the split tail of tiles with at
+// least kSplitMinTileSteps K steps; whether the tail is split is decided on
+// the device, where the live tile count is.
 template <Bwd kMode>
-int launch_bwd(const BwdArgs& p, int64_t total, hipStream_t s, const char* name) {
+int launch_bwd(BwdArgs p, int64_t total, hipStream_t s, const char* name, const GemmWorkspace& ws = {}) {
   if (total == 0) return ASTRAI_MOE_OK;
   if (total >= (1ll << 31)) return fail(ASTRAI_MOE_EINVAL, "%s: %lld tiles exceed the tile-index range", name,
                                         (long long)total);
   const int64_t grid = std::min<int64_t>(total, cu_count());
+  p.grid = (int)grid;
+  p.part = nullptr;
+  constexpr bool kSplit = kMode == Bwd::kDgradIn || kMode == Bwd::kDgradInAdd;
+  if (kSplit && ws.base != nullptr && p.K / kBK >= kSplitMinTileSteps &&
+      ws.bytes >= kSchedBytes + grid * (int64_t)sizeof(float) * kSplitUnitFloats)
+    p.part = reinterpret_cast<float*>(static_cast<char*>(ws.base) + kSchedBytes);
   hipLaunchKernelGGL((gemm_bwd_kernel<kMode>), dim3((unsigned)grid), dim3(BwdCfg::THREADS), 0, s, p);
-  return check_launch(name);
+  if (int rc = check_launch(name)) return rc;
+  if constexpr (kSplit) {
+    if (p.part == nullptr) return ASTRAI_MOE_OK;
+    hipLaunchKernelGGL((gemm_bwd_kernel<kMode, true>), dim3((unsigned)grid), dim3(BwdCfg::THREADS), 0, s, p);
+    if (int rc = check_launch(name)) return rc;
+    hipLaunchKernelGGL((bwd_split_reduce_kernel<kMode>), dim3((unsigned)((grid + 1) / 2)), dim3(512), 0, s, p);
+    return check_launch("bwd_split_reduce_kernel");
+  }
+  return ASTRAI_MOE_OK;
 }
 
 }  // namespace
@@ -650,7 +752,7 @@ int launch_dgrad_down(const void* dy, const int32_t* tiles, int64_t capacity, co
 }
 
 int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity, const void* const* w, int64_t k,
-                    int64_t n, const void* add, void* dx, hipStream_t s) {
+                    int64_t n, const void* add, void* dx, hipStream_t s, const GemmWorkspace& ws) {
   BwdArgs p{};
   p.a0 = static_cast<const bf16_t*>(d);
   p.w0 = w;
@@ -662,8 +764,8 @@ int launch_dgrad_in(const void* d, const int32_t* tiles, int64_t capacity, const
   p.n_tiles_n = (int)ceil_div(n, BwdCfg::BN);
   p.capacity = (int)capacity;
   if (add != nullptr)
-    return launch_bwd<Bwd::kDgradInAdd>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in_add>");
-  return launch_bwd<Bwd::kDgradIn>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in>");
+    return launch_bwd<Bwd::kDgradInAdd>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in_add>", ws);
+  return launch_bwd<Bwd::kDgradIn>(p, capacity * p.n_tiles_n, s, "gemm_bwd_kernel<dgrad_in>", ws);
 }
 
 int launch_wgrad(const void* a, const void* b, const int32_t* offsets, int n_experts, int64_t m, int64_t n,

@@ -356,50 +356,6 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
   }
 }
 
-// The streaming kernels' persistent walk, with the last round's tiles split
-// along K. After R whole rounds of the G workgroups, L = total mod G tiles
-// are left; run whole, they would hold L compute units for a full tile time
-// while the other G - L idle (measured at the Mixtral-shaped down GEMM: 32
-// tiles left after 8 rounds, 1.5 % of the work, cost 7.8 % of its time).
-// When a partial-sum buffer is given and L <= G / 2, each of those tiles is
-// cut into S = min(G / L, KT / kSplitMinSteps) ranges of K steps; the L * S
-// work units take the last round's slots (one per workgroup), each stores its
-// fp32 accumulators, and split_reduce_kernel sums a tile's S partials in
-// slice order and runs the tile's epilogue. Work items are indexed like
-// tiles: item i < full is logical tile i, item full + u is unit u (tile
-// full + u / S, slice u % S).
-constexpr int kSplitMinSteps = 8;
-// Tiles of fewer K steps are never split: the reduce launch and the partial
-// sums' traffic (~15 us at 16 tiles) cost about what splitting a short tile
-// saves (the fine-grained shape's 22-step down tiles take ~31 us).
-constexpr int kSplitMinTileSteps = 64;
-constexpr int kSplitUnitFloats = kMfmaBigBM * 256;  // fp32 accumulators of one 256 x 256 tile
-
-template <int GM>
-struct SplitWalk : TileWalk<GM> {
-  int full, S, KT;
-  __device__ SplitWalk(const int32_t* tiles, int capacity, int n_tiles_n, int KT_, bool split, int G_ = 0)
-      : TileWalk<GM>(tiles, capacity, n_tiles_n, G_), full(this->total), S(1), KT(KT_) {
-    if (split) {
-      const int L = this->total % this->G;
-      const int s = (L > 0 && 2 * L <= this->G) ? min(this->G / L, KT / kSplitMinSteps) : 1;
-      if (s >= 2) S = s, full = this->total - L;
-    }
-  }
-  __device__ int items() const { return full + (this->total - full) * S; }
-  // item `i` (< items()): its tile, K steps [k0, k1) and tail unit (-1: the whole tile)
-  __device__ void item(int i, int& mt, int& nt, int& k0, int& k1, int& unit) const {
-    if (i < full) {
-      this->decode(i, mt, nt);
-      k0 = 0, k1 = KT, unit = -1;
-      return;
-    }
-    const int u = i - full, s = u % S;
-    this->decode(full + u / S, mt, nt);
-    k0 = s * KT / S, k1 = (s + 1) * KT / S, unit = u;
-  }
-};
-
 // The order in which one workgroup takes its work items. Items below `dyn`
 // are dealt statically: the workgroup's slot, then every G-th item. Given a
 // scheduling block (`sched`, its counter cleared before the launch), the
@@ -489,19 +445,6 @@ struct StepCursor {
     return live;
   }
 };
-
-// A tail unit's fp32 accumulators, wave by wave in the accumulator layout:
-// part[unit][wave][i][j][lane] as 16-byte vectors (one 1 KB store per wave
-// and 16x16 tile).
-template <int MT16, int NT16>
-__device__ __forceinline__ void store_partial(const f32x4_t (&acc)[MT16][NT16], float* part, int unit, int wave,
-                                              int lane) {
-  f32x4_t* p = reinterpret_cast<f32x4_t*>(part) + ((int64_t)unit * 8 + wave) * (MT16 * NT16 * 64) + lane;
-#pragma unroll
-  for (int i = 0; i < MT16; ++i)
-#pragma unroll
-    for (int j = 0; j < NT16; ++j) p[(i * NT16 + j) * 64] = acc[i][j];
-}
 
 // kGather: A is x and the activation rows are gathered through row_src (the
 // permutation's source tokens).

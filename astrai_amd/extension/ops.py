@@ -152,7 +152,8 @@ def expert_weight_table(weights: Sequence[torch.Tensor], shape: tuple[int, int])
 
     Every weight must be a contiguous ``[out, in] == shape`` tensor on one
     device with one dtype, starting on a 16-byte boundary when its rows are a
-    multiple of 16 bytes; the kernels read them in place.
+    multiple of 16 bytes; the kernels read them in place, and the table keeps
+    references to them.
     """
     if len(weights) == 0:
         raise ValueError("no expert weights")
@@ -166,7 +167,11 @@ def expert_weight_table(weights: Sequence[torch.Tensor], shape: tuple[int, int])
         # rows of a multiple of 16 bytes are read with 16-byte vector loads
         if (w.shape[1] * w.element_size()) % 16 == 0 and w.data_ptr() % 16 != 0:
             raise ValueError(f"expert weight {i} must start on a 16-byte boundary (its rows are read 16 bytes at a time)")
-    return torch.tensor([w.data_ptr() for w in weights], dtype=torch.int64).to(dev)
+    table = torch.tensor([w.data_ptr() for w in weights], dtype=torch.int64).to(dev)
+    # the table holds raw addresses: it keeps the weights alive, so that a
+    # table outliving the caller's list never points at freed memory
+    table._astrai_weights = tuple(weights)
+    return table
 
 
 def moe_route(logits: torch.Tensor, top_k: int) -> RouteResult:
@@ -600,8 +605,10 @@ def moe_gemm_dgrad_down(dy: torch.Tensor, tiles: torch.Tensor, w_down: torch.Ten
 
 
 def moe_gemm_dgrad_gate_up(dg: torch.Tensor, du: torch.Tensor, tiles: torch.Tensor, w_gate: torch.Tensor,
-                           w_up: torch.Tensor, n_experts: int, dim: int) -> torch.Tensor:
-    """``dx_perm = dg . W_gate + du . W_up`` per expert."""
+                           w_up: torch.Tensor, n_experts: int, dim: int, balance: bool = True) -> torch.Tensor:
+    """``dx_perm = dg . W_gate + du . W_up`` per expert. ``balance``: a
+    partial last round of long 256-row tiles is split along K (False: every
+    tile runs whole)."""
     _require_gpu(dg, "dg", 2)
     code = _dtype_code(dg, "dg")
     n_rows, dim_ffn = dg.shape
@@ -610,9 +617,10 @@ def moe_gemm_dgrad_gate_up(dg: torch.Tensor, du: torch.Tensor, tiles: torch.Tens
     _require_table(w_gate, "w_gate", n_experts, dg)
     _require_table(w_up, "w_up", n_experts, dg)
     dx = torch.empty(n_rows, dim, dtype=dg.dtype, device=dg.device)
+    ws, ws_bytes = _workspace(dg, dim, dim_ffn, bm, down=True, balance=balance)
     _lib_call("astrai_moe_gemm_dgrad_gate_up", dg.data_ptr(), du.data_ptr(), tiles.data_ptr(), tiles.numel(),
               w_gate.data_ptr(), w_up.data_ptr(), code, n_rows, n_experts, dim_ffn, dim, bm,
-              dx.data_ptr(), _stream(dg))
+              dx.data_ptr(), _ptr(ws), ws_bytes, _stream(dg))
     return dx
 
 

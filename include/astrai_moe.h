@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 7
+#define ASTRAI_MOE_ABI_VERSION 8
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -404,6 +404,14 @@ int astrai_moe_gemm_dgrad_down(const void* dy, const int32_t* tiles,
  * Grouped dgrad of the gate and up projections:
  *   dx_perm = round(round(dg . W_gate[e]) + round(du . W_up[e]))   [n_rows, dim] dtype
  * (autograd's rounding: each linear's input gradient, then their sum).
+ * workspace: as the down GEMM's (astrai_moe_gemm_workspace_bytes(1) bytes,
+ *   16-byte aligned, nothing to initialise; NULL / 0: none). With it, a
+ *   partial last round of 256-row tiles of at least 64 K steps is split
+ *   along K and the slices' fp32 sums are added in a fixed order: the same
+ *   result on every call, but those tiles' sums are associated differently
+ *   from the unsplit kernel's, and which tiles form the tail depends on the
+ *   device's compute-unit count. Calls sharing a workspace must be ordered
+ *   on one stream.
  */
 int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du,
                                   const int32_t* tiles, int64_t tiles_len,
@@ -411,7 +419,8 @@ int astrai_moe_gemm_dgrad_gate_up(const void* dg, const void* du,
                                   const void* const* w_up, int dtype,
                                   int64_t n_rows, int n_experts,
                                   int64_t dim_ffn, int64_t dim, int block_m,
-                                  void* dx_perm, void* stream);
+                                  void* dx_perm, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
 
 /*
  * Per-expert weight gradient: dw[e] = a[rows of e]^T . b[rows of e], the rows

@@ -156,3 +156,68 @@ def test_wgrad_rows_not_multiple_of_64(gpu):
             continue
         ref = a[offs[e]:offs[e + 1]].float().T @ b[offs[e]:offs[e + 1]].float()
         _close(dw[e], ref, f"expert {e} ({c} rows)")
+
+
+def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
+    """(L, S): tail tiles of the last round and their K slices, as the dgrad
+    kernels decide them (S = 1: the tail runs whole; tiles of fewer than 64 K
+    steps never split)."""
+    if ksteps < 64:
+        return 0, 1
+    grid = min(capacity * n_tiles_n, cus)
+    left = (n_live * n_tiles_n) % grid
+    s = min(grid // left, ksteps // 8) if 0 < left and 2 * left <= grid else 1
+    return (left, s) if s >= 2 else (0, 1)
+
+
+def _diff_blocks(a, b, tl, n_live):
+    """(row tile, column tile) blocks in which a and b differ."""
+    row_tile = torch.full((a.shape[0],), -1, dtype=torch.long)
+    for i in range(n_live):
+        r0, end = tl[5 + 3 * i], tl[6 + 3 * i]
+        row_tile[r0:min(r0 + 256, end)] = i
+    rows, cols = (a != b).cpu().nonzero(as_tuple=True)
+    return {(int(row_tile[r]), int(c) // 256) for r, c in zip(rows.tolist(), cols.tolist())}
+
+
+@pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
+    (4096, 8, 2, 512, 4096),  # ~35 row tiles x 2, K 4096: 70 tiles on 78 workgroups, too many to split
+    (11264, 8, 2, 1024, 4096),  # ~92 x 4 = ~368 tiles on 256 workgroups: ~112 left, split 2 ways
+    (16384, 8, 2, 512, 4096),  # ~132 x 2 = ~264 tiles: a short last round split 8 ways
+    (16384, 8, 2, 2048, 1408),  # 22 K steps: the tail runs whole
+])
+def test_dgrad_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
+    """The dgrad_in GEMMs (dx_perm = dg . W_gate + du . W_up) with their
+    workspace (a partial last round of tiles of 64+ K steps split along K, the
+    slices' fp32 sums added in slice order by a reduce launch that runs the
+    tile's epilogue) against the same GEMMs run whole: dx differs only inside
+    the predicted tail tiles, and there within the layer's tolerance."""
+    perm, weights, (tg, tu, td), gen = _setup(gpu, n_tok, n_exp, top_k, dim, dim_ffn, seed=5)
+    E = n_exp
+    _, gu = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, E, dim_ffn)
+    dy = (torch.randn(perm.x_perm.shape[0], dim, generator=gen, device=gpu) * 0.5).to(BF)
+    dg, du = ops.moe_gemm_dgrad_down(dy, perm.tiles, td, gu, E)
+    dx = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim)
+    dx_w = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim, balance=False)
+    torch.cuda.synchronize()
+    tl = perm.tiles.cpu().tolist()
+    n_live, capacity = tl[0], (len(tl) - 4) // 3
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    left, s = _tail_split(n_live, -(-dim // 256), capacity, dim_ffn // 64, cus)
+    print(f"{n_live} row tiles: dgrad_in tail {left} tiles, {s} slices", flush=True)
+    blocks = _diff_blocks(dx, dx_w, tl, n_live)
+    assert len(blocks) <= left, (len(blocks), left)
+    if s == 1:
+        assert torch.equal(dx, dx_w)
+    else:
+        # the split path ran: reassociated fp32 sums change some bf16 roundings
+        assert blocks
+    _close(dx, dx_w, "dx")
+    offs = perm.expert_offsets.tolist()
+    wg, wu, _ = weights
+    for e in range(E):
+        a, b = offs[e], offs[e + 1]
+        if a == b:
+            continue
+        ref = (dg[a:b].float() @ wg[e].float()).to(BF).float() + (du[a:b].float() @ wu[e].float()).to(BF).float()
+        _close(dx[a:b], ref, f"e{e} dx")

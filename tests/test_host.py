@@ -213,9 +213,13 @@ def test_abi_rejects_bad_arguments_with_message():
     assert rc == -1 and "workspace must be 16-byte aligned" in loader.last_error()
     rc = lib.astrai_moe_gemm_down_train(16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 16, 8, 1 << 20, None)
     assert rc == -1 and "workspace must be 16-byte aligned" in loader.last_error()
+    rc = lib.astrai_moe_gemm_dgrad_gate_up(16, 16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 16, -1, None)
+    assert rc == -1 and "negative workspace size" in loader.last_error()
+    rc = lib.astrai_moe_gemm_dgrad_gate_up(16, 16, 16, 7, 16, 16, 1, 4, 2, 256, 256, 256, 16, 8, 1 << 20, None)
+    assert rc == -1 and "workspace must be 16-byte aligned" in loader.last_error()
     rc = lib.astrai_moe_gemm_dgrad_down(1, 1, 7, 1, None, 1, 4, 2, 256, 128, 256, 1, 1, None)
     assert rc == -1 and "null" in loader.last_error()
-    rc = lib.astrai_moe_gemm_dgrad_gate_up(1, 1, 1, 7, 1, 1, 1, 4, 2, 128, 256, 64, 1, None)
+    rc = lib.astrai_moe_gemm_dgrad_gate_up(1, 1, 1, 7, 1, 1, 1, 4, 2, 128, 256, 64, 1, None, 0, None)
     assert rc == -1 and "256-row tile list" in loader.last_error()
     rc = lib.astrai_moe_row_grad(1, 1, 1, 1, 1, 4, 0, 1, 1, None)
     assert rc == -1 and "dim must be" in loader.last_error()
