@@ -153,10 +153,10 @@ struct TileWalk {
 // When a partial-sum buffer is given and L <= G / 2, each of those tiles is
 // cut into S = min(G / L, KT / kSplitMinSteps) ranges of K steps; the L * S
 // work units take the last round's slots (one per workgroup), each stores its
-// fp32 accumulators, and split_reduce_kernel sums a tile's S partials in
-// slice order and runs the tile's epilogue (the backward's dgrad GEMMs reduce
-// theirs the same way). Work items are indexed like
-// tiles: item i < full is logical tile i, item full + u is unit u (tile
+// fp32 accumulators, and a reduce kernel (split_reduce_kernel of the forward
+// down GEMM, bwd_split_reduce_kernel of the dgrad_in GEMMs) sums a tile's S
+// partials in slice order and runs the tile's epilogue. Work items are indexed
+// like tiles: item i < full is logical tile i, item full + u is unit u (tile
 // full + u / S, slice u % S).
 constexpr int kSplitMinSteps = 8;
 // Tiles of fewer K steps are never split: the reduce launch and the partial

@@ -40,7 +40,11 @@
 // one barrier per 64-K step, the next step's first fragments prefetched
 // across tile boundaries. dgrad walks the forward's 256-row tile list; wgrad
 // walks (expert, M tile, N tile) with K = the expert's rows, rows past the
-// expert's end read from a zero row.
+// expert's end read from a zero row. Given a workspace, the dgrad_in GEMMs
+// split a partial last round along K: a second launch of the same kernel
+// (kTail) runs the slices into fp32 partial tiles, and
+// bwd_split_reduce_kernel adds each tile's slices in order and runs its
+// epilogue.
 #include "mfma_tile.h"
 
 #include <type_traits>
