@@ -184,6 +184,7 @@ def _diff_blocks(a, b, tl, n_live):
     (4096, 8, 2, 512, 4096),  # ~35 row tiles x 2, K 4096: 70 tiles on 78 workgroups, too many to split
     (11264, 8, 2, 1024, 4096),  # ~92 x 4 = ~368 tiles on 256 workgroups: ~112 left, split 2 ways
     (16384, 8, 2, 512, 4096),  # ~132 x 2 = ~264 tiles: a short last round split 8 ways
+    (18432, 8, 2, 1024, 4096),  # ~148 x 4 = ~592 tiles: 2 whole rounds, ~80 left split 3 ways
     (16384, 8, 2, 2048, 1408),  # 22 K steps: the tail runs whole
 ])
 def test_dgrad_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
