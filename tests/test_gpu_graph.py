@@ -93,6 +93,18 @@ def test_graph_shapes(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, n_tok):
     _check_graph(layer, x)
 
 
+@pytest.mark.parametrize("dim,dim_ffn,n_tok", [
+    (3072, 1024, 8192),  # gate/up: 48 K steps, the last tenth of ~544 tiles claimed at run time
+    (1024, 4096, 8192),  # down: 64 K steps, claims and a split last round (fp32 partials, ordered reduce)
+])
+def test_graph_run_time_claims_and_split_tail(gpu, dim, dim_ffn, n_tok):
+    # the claim counter is cleared by a kernel of the capture on every replay,
+    # and the workspace comes from the graph's own pool
+    layer = _layer(gpu, dim, dim_ffn, 8, 1, 2, torch.bfloat16)
+    x = torch.randn(1, n_tok, dim, device=gpu).to(torch.bfloat16)
+    _check_graph(layer, x)
+
+
 def test_graph_packed_weights(gpu):
     # the packed copy is built by the warm-up call, outside the capture
     layer = _layer(gpu, 512, 256, 16, 1, 4, torch.bfloat16)

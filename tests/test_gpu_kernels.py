@@ -280,6 +280,22 @@ def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_
                 torch.testing.assert_close(y_unw[a:b], F.linear(h[a:b], w.down), **BF16_TOL)
 
 
+
+def test_weight_table_keeps_its_weights_alive(gpu):
+    """A pointer table outliving the caller's list of weights still owns them:
+    their storage is not handed to new tensors while the table lives."""
+    w = [torch.randn(256, 128, device=gpu).to(torch.bfloat16) for _ in range(3)]
+    ref = [t.clone() for t in w]
+    table = ops.expert_weight_table(w, (256, 128))
+    ptrs = {t.data_ptr() for t in w}
+    del w
+    junk = [torch.full((256, 128), float("nan"), device=gpu, dtype=torch.bfloat16) for _ in range(6)]
+    assert not ptrs & {j.data_ptr() for j in junk}
+    kept = table._astrai_weights
+    assert all(torch.equal(a, b) for a, b in zip(kept, ref))
+    assert [t.data_ptr() for t in kept] == table.cpu().tolist()
+
+
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn", [
     (2048, 8, 2, 1024, 1536),  # 256-row tiles
     (300, 16, 4, 512, 256),  # 64-row tiles
