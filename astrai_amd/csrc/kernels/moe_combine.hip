@@ -65,7 +65,7 @@ struct Vec {  // VW elements of T as one load / store unit
 
 template <typename T, int VW, int KMAX, int U, bool NT>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
-    const T* __restrict__ y, const int32_t* __restrict__ token_pos,
+    const T* __restrict__ y, const int32_t* __restrict__ token_pos, const T* __restrict__ row_w,
     const T* __restrict__ shared, int n_shared, float inv_shared,
     int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, T* __restrict__ out) {
   const int lane = threadIdx.x & 63;
@@ -96,6 +96,11 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
       rows[r] = (m && p < n_tokens * top_k) ? p : -1;
     }
   }
+  // row_w: y holds unweighted rows; each is scaled by its routing weight and
+  // rounded before the sum, as the down GEMM's epilogue does (mlp.py:97)
+  float wr[KMAX];
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) wr[r] = (row_w != nullptr && rows[r] >= 0) ? Elem<T>::to_f32(row_w[rows[r]]) : 1.0f;
 
   const int64_t v_end = min(nvec, (seg + 1) * seg_units);
   for (int64_t v0 = seg * seg_units + lane; v0 < v_end; v0 += 64 * U) {
@@ -117,7 +122,11 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
       for (int r = 0; r < KMAX; ++r)
         if (rows[r] >= 0)
 #pragma unroll
-          for (int j = 0; j < VW; ++j) acc[j] = Elem<T>::round(acc[j] + Elem<T>::to_f32(in[r][u].v[j]));
+          for (int j = 0; j < VW; ++j) {
+            float val = Elem<T>::to_f32(in[r][u].v[j]);
+            if (row_w != nullptr) val = Elem<T>::round(val * wr[r]);
+            acc[j] = Elem<T>::round(acc[j] + val);
+          }
       float sh[VW];
 #pragma unroll
       for (int j = 0; j < VW; ++j) sh[j] = 0.0f;
@@ -139,30 +148,32 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(
 }
 
 template <typename T, int VW, int KMAX, int U, bool NT>
-void launch_combine_cfg(const void* y, const int32_t* token_pos, const void* shared, int n_shared, float inv_shared,
-                        int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid, void* out,
-                        hipStream_t s) {
+void launch_combine_cfg(const void* y, const int32_t* token_pos, const void* row_w, const void* shared, int n_shared,
+                        float inv_shared, int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid,
+                        void* out, hipStream_t s) {
   hipLaunchKernelGGL((combine_kernel<T, VW, KMAX, U, NT>), dim3((unsigned)grid), dim3(kCombineThreads), 0, s,
-                     static_cast<const T*>(y), token_pos, static_cast<const T*>(shared), n_shared, inv_shared,
+                     static_cast<const T*>(y), token_pos, static_cast<const T*>(row_w), static_cast<const T*>(shared),
+                     n_shared, inv_shared,
                      n_tokens, top_k, dim, seg_units, static_cast<T*>(out));
 }
 
 template <typename T, int VW>
-void dispatch_k(const void* y, const int32_t* token_pos, const void* shared, int n_shared, float inv_shared,
-                int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid, void* out, hipStream_t s) {
+void dispatch_k(const void* y, const int32_t* token_pos, const void* row_w, const void* shared, int n_shared,
+                float inv_shared, int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid, void* out,
+                hipStream_t s) {
   if (top_k <= 2)
-    launch_combine_cfg<T, VW, 2, 2, true>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units,
-                                          grid, out, s);
+    launch_combine_cfg<T, VW, 2, 2, true>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim,
+                                          seg_units, grid, out, s);
   else if (top_k <= 8)
-    launch_combine_cfg<T, VW, 8, 2, false>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim,
+    launch_combine_cfg<T, VW, 8, 2, false>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim,
                                            seg_units, grid, out, s);
   else
-    launch_combine_cfg<T, VW, ASTRAI_MOE_MAX_TOPK, 1, false>(y, token_pos, shared, n_shared, inv_shared, n_tokens,
-                                                            top_k, dim, seg_units, grid, out, s);
+    launch_combine_cfg<T, VW, ASTRAI_MOE_MAX_TOPK, 1, false>(y, token_pos, row_w, shared, n_shared, inv_shared,
+                                                            n_tokens, top_k, dim, seg_units, grid, out, s);
 }
 
 template <typename T>
-int launch_combine(const void* y, const int32_t* token_pos, const void* shared,
+int launch_combine(const void* y, const int32_t* token_pos, const void* row_w, const void* shared,
                    int n_shared, int64_t n_tokens, int top_k, int64_t dim,
                    void* out, hipStream_t s) {
   const float inv_shared = n_shared > 0 ? 1.0f / (float)n_shared : 0.0f;
@@ -180,9 +191,11 @@ int launch_combine(const void* y, const int32_t* token_pos, const void* shared,
   const int64_t grid = ceil_div(waves, kWavesPerBlock);
   if (grid >= (1ll << 31)) return fail(ASTRAI_MOE_EINVAL, "combine: too many tokens");
   if (vec)
-    dispatch_k<T, kVW>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units, grid, out, s);
+    dispatch_k<T, kVW>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units, grid, out,
+                       s);
   else
-    dispatch_k<T, 1>(y, token_pos, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units, grid, out, s);
+    dispatch_k<T, 1>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim, seg_units, grid, out,
+                     s);
   return check_launch("combine_kernel");
 }
 
@@ -191,7 +204,7 @@ int launch_combine(const void* y, const int32_t* token_pos, const void* shared,
 
 using namespace astrai_moe;
 
-extern "C" int astrai_moe_combine(const void* y, const int32_t* token_pos,
+extern "C" int astrai_moe_combine(const void* y, const int32_t* token_pos, const void* row_w,
                                   const void* shared, int n_shared, int dtype,
                                   int64_t n_tokens, int top_k, int64_t dim,
                                   void* out, void* stream) {
@@ -207,8 +220,8 @@ extern "C" int astrai_moe_combine(const void* y, const int32_t* token_pos,
                  "combine: n_shared must be >= 0 with a buffer when > 0");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == ASTRAI_MOE_BF16)
-    return launch_combine<bf16_t>(y, token_pos, shared, n_shared, n_tokens, top_k, dim, out, s);
+    return launch_combine<bf16_t>(y, token_pos, row_w, shared, n_shared, n_tokens, top_k, dim, out, s);
   if (dtype == ASTRAI_MOE_F32)
-    return launch_combine<float>(y, token_pos, shared, n_shared, n_tokens, top_k, dim, out, s);
+    return launch_combine<float>(y, token_pos, row_w, shared, n_shared, n_tokens, top_k, dim, out, s);
   return fail(ASTRAI_MOE_EINVAL, "combine: unsupported dtype %d", dtype);
 }

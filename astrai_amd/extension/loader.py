@@ -30,7 +30,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 KERNEL_NAMES = ["moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_down", "moe_combine"]
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 LIB_PATH = Path(os.environ.get("ASTRAI_MOE_LIB", Path(__file__).resolve().parent / "libastrai_moe.so"))
 
 _c_i32p = ctypes.POINTER(ctypes.c_int32)
@@ -59,7 +59,7 @@ _SIGNATURES: dict[str, tuple] = {
     "astrai_moe_gemm_down": (_int, [_vp, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int, _vp, _vp, _i64,
                                     _vp]),
     "astrai_moe_gemm_workspace_bytes": (_i64, [_int]),
-    "astrai_moe_combine": (_int, [_vp, _vp, _vp, _int, _int, _i64, _int, _i64, _vp, _vp]),
+    "astrai_moe_combine": (_int, [_vp, _vp, _vp, _vp, _int, _int, _i64, _int, _i64, _vp, _vp]),
     "astrai_moe_gemm_gate_up_gather": (_int, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _int, _i64, _int, _i64, _i64, _int,
                                               _vp, _vp, _i64, _vp]),
     "astrai_moe_pack_gate_up": (_int, [_vp, _vp, _int, _i64, _i64, _vp, _vp]),

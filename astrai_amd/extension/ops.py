@@ -407,9 +407,13 @@ def moe_pack_down(w_down: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def moe_combine(y: torch.Tensor, token_pos: torch.Tensor, shared: torch.Tensor | None = None) -> torch.Tensor:
+def moe_combine(y: torch.Tensor, token_pos: torch.Tensor, shared: torch.Tensor | None = None,
+                row_w: torch.Tensor | None = None) -> torch.Tensor:
     """out = mean(shared experts) + sum over experts (ascending) of y rows
-    (mlp.py:89, :98, :77, :71)."""
+    (mlp.py:89, :98, :77, :71). ``row_w`` (the permuted rows' routing
+    weights, ``sorted_w``): y holds unweighted rows, each scaled by its
+    weight and rounded before the sum (the same result as combining the
+    weighted down GEMM's rows)."""
     fn = _kernel("moe_combine")
     _require_gpu(y, "y", 2)
     code = _dtype_code(y, "y")
@@ -424,10 +428,14 @@ def moe_combine(y: torch.Tensor, token_pos: torch.Tensor, shared: torch.Tensor |
         if shared.shape[1:] != (n_tokens, dim) or shared.dtype != y.dtype:
             raise ValueError("shared must be [n_shared, n_tokens, dim] of y's dtype")
         n_shared = shared.shape[0]
+    if row_w is not None:
+        _require_gpu(row_w, "row_w", 1)
+        if row_w.shape[0] != n_tokens * top_k or row_w.dtype != y.dtype:
+            raise ValueError("row_w must hold n_tokens * top_k weights of y's dtype")
     out = torch.empty(n_tokens, dim, dtype=y.dtype, device=y.device)
     _check(
-        fn(y.data_ptr(), token_pos.data_ptr(), _ptr(shared), n_shared, code, n_tokens, top_k, dim, out.data_ptr(),
-           _stream(y)),
+        fn(y.data_ptr(), token_pos.data_ptr(), _ptr(row_w), _ptr(shared), n_shared, code, n_tokens, top_k, dim,
+           out.data_ptr(), _stream(y)),
         "moe_combine",
     )
     return out

@@ -69,8 +69,10 @@ class RoutedExperts(torch.autograd.Function):
         bm = ops.train_block_m(dim, dim_ffn, x.dtype)
         perm = ops.moe_permute(route, x, n_experts, bm)
         h, gu = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_experts, dim_ffn)
-        y, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_experts, dim)
-        out = ops.moe_combine(y, perm.token_pos)
+        # the down GEMM without routing weights gives the unweighted rows the
+        # backward keeps; the combine applies the weights (same rounding)
+        y_unw = ops.moe_gemm_down(h, perm.tiles, td, None, n_experts, dim, bm)
+        out = ops.moe_combine(y_unw, perm.token_pos, row_w=perm.sorted_w)
         # which experts got rows, for the backward: copied to pinned host
         # memory now, so that the backward reads it without waiting for its
         # own kernels

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 8
+#define ASTRAI_MOE_ABI_VERSION 9
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -321,12 +321,18 @@ int astrai_moe_gemm_down_packed(const void* h, const int32_t* tiles,
  *
  *   y          [n_tokens * top_k, dim]  dtype, from astrai_moe_gemm_down
  *   token_pos  [n_tokens * top_k]       int32, from astrai_moe_permute
+ *   row_w      [n_tokens * top_k]       dtype per permuted row (sorted_w), or
+ *              NULL. Given, y holds the unweighted rows (the down GEMM run
+ *              without row weights) and each is scaled by its weight and
+ *              rounded before the sum, as the weighted down GEMM would: the
+ *              same result, with one output fewer for a training forward
+ *              that keeps the unweighted rows anyway.
  *   shared     [n_shared, n_tokens, dim] dtype: each shared expert's output
  *              (NULL when n_shared == 0: the reference's zeros_like,
  *              mlp.py:75-76)
  *   out        [n_tokens, dim]          dtype
  */
-int astrai_moe_combine(const void* y, const int32_t* token_pos,
+int astrai_moe_combine(const void* y, const int32_t* token_pos, const void* row_w,
                        const void* shared, int n_shared, int dtype,
                        int64_t n_tokens, int top_k, int64_t dim, void* out,
                        void* stream);

@@ -510,6 +510,12 @@ def test_combine_bit_exact(gpu, n_tok, n_exp, top_k, dim, n_shared, dtype):
     ref = sh + ref
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+    # unweighted rows and their routing weights: each row scaled and rounded
+    # first (mlp.py:97's y * w), then the same sum
+    out_w = ops.moe_combine(y, perm.token_pos, shared, row_w=perm.sorted_w)
+    y_w = (y.float() * perm.sorted_w.float().unsqueeze(-1)).to(dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(out_w, ops.moe_combine(y_w, perm.token_pos, shared))
 
 
 @pytest.mark.parametrize("n_tok,dim,dim_ffn,dtype", [

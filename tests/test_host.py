@@ -173,7 +173,7 @@ def test_abi_rejects_bad_arguments_with_message():
     rc = lib.astrai_moe_permute(None, None, None, None, 1, 10, 8, 2, 16, 64, None, None, None, None, None,
                                 None, 3, None, None)
     assert rc == -1 and "tile list" in loader.last_error()
-    rc = lib.astrai_moe_combine(1, 1, None, 2, 1, 4, 2, 8, 1, None)
+    rc = lib.astrai_moe_combine(1, 1, None, None, 2, 1, 4, 2, 8, 1, None)
     assert rc == -1 and "n_shared" in loader.last_error()
     rc = lib.astrai_moe_pack_gate_up(None, None, 0, 128, 64, None, None)
     assert rc == -1 and "bf16 only" in loader.last_error()
@@ -232,7 +232,7 @@ def test_abi_rejects_bad_arguments_with_message():
     assert lib.astrai_moe_gemm_wgrad(None, None, None, 1, 0, 2, 16, 16, None, None) == 0
     # Empty inputs are a valid no-op.
     assert lib.astrai_moe_route(None, 1, 0, 8, 2, None, None, None, None) == 0
-    assert lib.astrai_moe_combine(None, None, None, 0, 1, 0, 2, 8, None, None) == 0
+    assert lib.astrai_moe_combine(None, None, None, None, 0, 1, 0, 2, 8, None, None) == 0
 
 
 def test_tile_list_len_bounds_the_tile_count():
