@@ -30,11 +30,13 @@ __device__ inline float sigmoid_precise(float x) { return 1.0f / (1.0f + expf(-x
 
 // C[rows, N] = A[rows, K] . W_e[K, N] for every row tile of the tile list
 // (e = the tile's expert), W_e row-major [K, N]. Grid: (tile-list capacity,
-// column tiles); each block walks its row tile in 64-row steps.
+// column tiles); each block walks its row tile in 64-row steps. E0 and C0
+// may be the same buffer (kDgradInAdd adds in place: each element is read
+// and then written by the same thread), so neither is declared restrict.
 template <typename T, Nn kMode>
 __global__ __launch_bounds__(kThreads) void gemm_nn_generic_kernel(
     const T* __restrict__ A, const int32_t* __restrict__ tiles, const void* const* __restrict__ W,
-    const T* __restrict__ E0, int64_t K, int64_t N, T* __restrict__ C0, T* __restrict__ C1) {
+    const T* E0, int64_t K, int64_t N, T* C0, T* C1) {
   const int tile = blockIdx.x;
   const int n_live = min(tiles[0], tiles[2]);
   if (tile >= n_live) return;

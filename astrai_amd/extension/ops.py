@@ -33,6 +33,9 @@ MAX_EXPERTS = 1024
 MAX_TOPK = 32
 TILE_HEADER = 4
 TILE_STRIDE = 3
+# K steps (of 64) per tile from which the 256-row down-sized GEMMs split a
+# partial last round along K (kSplitMinTileSteps in mfma_tile.h)
+SPLIT_MIN_STEPS = 64
 
 _DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1}
 
@@ -240,7 +243,10 @@ def _workspace(a: torch.Tensor, dim: int, dim_ffn: int, block_m: int, down: bool
     ``balance=False``: none, every tile dealt in advance and run whole."""
     if not balance or block_m != 256 or a.dtype != torch.bfloat16 or not matrix_core_supported(dim, dim_ffn, a.dtype):
         return None, 0
-    nbytes = int(loader.library().astrai_moe_gemm_workspace_bytes(1 if down else 0))
+    # the partial sums serve only tiles of SPLIT_MIN_STEPS K steps or more
+    # (K = dim_ffn for the down-sized users): below that, the scheduling part
+    split = down and dim_ffn // 64 >= SPLIT_MIN_STEPS
+    nbytes = int(loader.library().astrai_moe_gemm_workspace_bytes(1 if split else 0))
     return torch.empty(nbytes, dtype=torch.uint8, device=a.device), nbytes
 
 

@@ -25,7 +25,11 @@ Prints one JSON line:
   parity          the timed configuration's output, routing and permutation
                   against the oracle on the same device (outside the timed
                   region): routing and permutation bit-exact flags, the plain
-                  allclose pass fraction and the max normalised error
+                  allclose pass fraction and the max normalised error; and
+                  the layer's output and the oracle's against an fp64 truth
+                  of the same inputs (every intermediate unrounded): each
+                  one's plain-tolerance failures, max normalised and RMS
+                  error (truth_*)
 """
 
 from __future__ import annotations
@@ -187,7 +191,8 @@ def parity_leg(layer, x, w, ops) -> dict:
         route = ops.moe_route(layer.router(x_flat), w.top_k)
         block_m = ops.select_block_m(w.n_tokens, w.n_experts, w.top_k, w.dim, w.dim_ffn, w.dtype)
         perm = ops.moe_permute(route, x_flat, w.n_experts, block_m, copy_rows=False)
-        rep = P.layer_parity(layer, x, out, route.topk_idx, route.topk_w, perm.sorted_token, perm.expert_offsets)
+        rep = P.layer_parity(layer, x, out, route.topk_idx, route.topk_w, perm.sorted_token, perm.expert_offsets,
+                             truth_tokens=0)
     torch.cuda.synchronize()
     return rep
 

@@ -126,8 +126,7 @@ int astrai_moe_permute(const int32_t* topk_idx, const void* topk_w,
 /*
  * astrai_moe_permute without the chunk_base workspace, for callers that cannot
  * allocate device memory (code under graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). No counterpart in the reference: its
- * permutation (mlp.py:90-95) allocates through torch on every call.
+ * harnesses that forbid hipMalloc). No counterpart in the reference.
  * Same arguments, results (bit-identical) and errors as astrai_moe_permute,
  * minus chunk_base: the scan's scratch is a fixed array inside the library,
  * ASTRAI_MOE_NOALLOC_SCRATCH_INTS int32 per GPU, held from the first call on

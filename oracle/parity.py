@@ -21,6 +21,17 @@ What is compared (the reference being ``astrai/model/components/mlp.py:64-100``)
     each of the k expert terms summed into the element (at most 0 passes).
     Where expert terms cancel, the sum is small while each term carries its
     own rounding, so this is the bound that stays meaningful there.
+* with ``truth_tokens``, both outputs against an fp64 truth: the layer
+  evaluated from the same inputs (the same bf16 / fp32 activations and
+  weights, the reference's routing, which both paths share bit for bit) with
+  every intermediate kept in fp64, i.e. without the reference's rounding
+  points (``mlp.py:23-24, 96-98``). For the kernels' output and for the
+  reference's: the number of elements outside the plain tolerance around the
+  truth (``truth_fail_kernel`` / ``truth_fail_ref``), the max normalised
+  error and the RMS error. The elements where the kernels' output and the
+  reference's disagree beyond the plain tolerance are where either carries
+  its own bf16 roundings of cancelling expert terms; against the truth the
+  two paths must fail about equally often.
 """
 
 from __future__ import annotations
@@ -36,12 +47,57 @@ def tolerance(dtype: torch.dtype) -> tuple[float, float]:
     return (2e-2, 2e-3) if dtype == torch.bfloat16 else (1e-5, 1e-5)
 
 
+def truth_forward(x_flat: Tensor, topk_idx: Tensor, topk_w: Tensor, experts, shared) -> Tensor:
+    """The layer's output in fp64 from the same inputs: for every token,
+    ``sum_k w_k * down(up(x) * silu(gate(x)))`` over its routed experts (the
+    given routing and its renormalised weights, widened to fp64), plus the
+    mean of the shared experts, with no rounding of any intermediate. The
+    sum over experts runs in ascending expert order like the reference's
+    ``index_add_`` (mlp.py:89-98), which in fp64 no longer changes the result
+    at the tolerance in question. Returns ``[T, D]`` float64."""
+    out = torch.zeros(x_flat.shape, dtype=torch.float64, device=x_flat.device)
+
+    def mlp64(xe: Tensor, w) -> Tensor:
+        g = xe @ w.gate.double().T
+        u = xe @ w.up.double().T
+        return (u * (g * torch.sigmoid(g))) @ w.down.double().T
+
+    for e, w in enumerate(experts):
+        tok, slot = (topk_idx.long() == e).nonzero(as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        y = mlp64(x_flat[tok].double(), w)
+        out.index_add_(0, tok, y * topk_w[tok, slot].double().unsqueeze(-1))
+    if len(shared):
+        xs = x_flat.double()
+        out += sum(mlp64(xs, w) for w in shared) / len(shared)
+    return out
+
+
+def truth_errors(out: Tensor, ref: Tensor, truth: Tensor, dtype: torch.dtype) -> dict:
+    """Errors of the kernels' output ``out`` and the reference's ``ref``
+    against the fp64 ``truth`` (all ``[T, D]``): failures of the plain
+    tolerance around the truth, max normalised error and RMS error of each."""
+    rtol, atol = tolerance(dtype)
+    bound = atol + rtol * truth.abs()
+    rep = {"truth_elements": truth.numel()}
+    for name, t in (("kernel", out), ("ref", ref)):
+        err = (t.double() - truth).abs()
+        rep[f"truth_fail_{name}"] = int((err > bound).sum().item())
+        rep[f"truth_max_norm_err_{name}"] = (err / bound).max().item() if err.numel() else 0.0
+        rep[f"truth_rms_err_{name}"] = err.square().mean().sqrt().item() if err.numel() else 0.0
+    return rep
+
+
 def layer_parity(layer, x: Tensor, out: Tensor, topk_idx: Tensor | None = None, topk_w: Tensor | None = None,
-                 sorted_token: Tensor | None = None, expert_offsets: Tensor | None = None) -> dict:
+                 sorted_token: Tensor | None = None, expert_offsets: Tensor | None = None,
+                 truth_tokens: int | None = None) -> dict:
     """Compare ``out = layer(x)`` with the oracle evaluated on the layer's own
     parameters on x's device; optionally also the kernels' routing
     (``topk_idx [T, K]``, ``topk_w [T, K]``) and permutation
-    (``sorted_token [T K]``, ``expert_offsets [E + 1]``) for the same input."""
+    (``sorted_token [T K]``, ``expert_offsets [E + 1]``) for the same input,
+    and (``truth_tokens``: the first that many tokens, 0 or more than T for
+    all) both outputs against the fp64 truth (``truth_errors``)."""
     rtol, atol = tolerance(x.dtype)
     dim = x.shape[-1]
     x_flat = x.reshape(-1, dim)
@@ -77,4 +133,9 @@ def layer_parity(layer, x: Tensor, out: Tensor, topk_idx: Tensor | None = None, 
             same_rows = torch.equal(sorted_token.long(), tok)
             same_off = expert_offsets is None or torch.equal(expert_offsets.long(), offsets)
             report["permutation_bit_exact"] = bool(same_rows and same_off)
+        if truth_tokens is not None:
+            n = x_flat.shape[0] if truth_tokens <= 0 else min(truth_tokens, x_flat.shape[0])
+            truth = truth_forward(x_flat[:n], trace.topk_idx[:n], trace.topk_w[:n], experts, shared)
+            report.update(truth_errors(out.reshape(x_flat.shape)[:n], ref[:n], truth, x.dtype))
+            report["truth_tokens"] = n
     return report

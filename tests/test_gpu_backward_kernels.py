@@ -200,7 +200,14 @@ def test_dgrad_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn):
     dg, du = ops.moe_gemm_dgrad_down(dy, perm.tiles, td, gu, E)
     dx = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim)
     dx_w = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim, balance=False)
+    # the same calls again, bit for bit (the split tail's slices and their
+    # ordered reduce, and the whole-tile walk, are deterministic)
+    dg2, du2 = ops.moe_gemm_dgrad_down(dy, perm.tiles, td, gu, E)
+    dx2 = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim)
+    dx_w2 = ops.moe_gemm_dgrad_gate_up(dg, du, perm.tiles, tg, tu, E, dim, balance=False)
     torch.cuda.synchronize()
+    assert torch.equal(dg, dg2) and torch.equal(du, du2)
+    assert torch.equal(dx, dx2) and torch.equal(dx_w, dx_w2)
     tl = perm.tiles.cpu().tolist()
     n_live, capacity = tl[0], (len(tl) - 4) // 3
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count

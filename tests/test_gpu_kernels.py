@@ -14,6 +14,7 @@ import torch
 import torch.nn.functional as F
 
 from astrai_amd.extension import ops
+from astrai_amd.workloads import HEADLINE, WORKLOADS, make_layer
 from oracle import moe_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -188,6 +189,45 @@ def test_grouped_gemms_match_torch(gpu, n_tok, n_exp, top_k, dim, dim_ffn, dtype
         torch.testing.assert_close(y[a:b], y_ref, **tol)
 
 
+def test_grouped_gemms_at_the_mixtral_shape(gpu):
+    """The Mixtral-shaped workload's own activations, routing and expert
+    weights (D 4096, F 14336, 8 experts, top-2, 16384 tokens) through the
+    kernels the layer runs there: the gate/up GEMM gathering x through the
+    permutation (run-time claims engaged: 64 K steps per tile) and the down
+    GEMM with its workspace (224 K steps: claims and the split tail). Every
+    expert's h and y against F.linear at the reference's rounding points
+    (mlp.py:23-24, :97), every element within rtol 2e-2 / atol 2e-3."""
+    w = WORKLOADS[HEADLINE]
+    layer, x = make_layer(w, gpu)
+    E, D, Fd, K = w.n_experts, w.dim, w.dim_ffn, w.top_k
+    x2 = x.view(-1, D)
+    with torch.no_grad():
+        route = ops.moe_route(layer.router(x2), K)
+    bm = ops.select_block_m(x2.shape[0], E, K, D, Fd, x2.dtype)
+    assert bm == 256
+    perm = ops.moe_permute(route, x2, E, bm, copy_rows=False)
+    experts = layer.routed_experts
+    tg = ops.expert_weight_table([m.gate.weight for m in experts], (Fd, D))
+    tu = ops.expert_weight_table([m.up.weight for m in experts], (Fd, D))
+    td = ops.expert_weight_table([m.down.weight for m in experts], (D, Fd))
+    h = ops.moe_gemm_gate_up_gather(x2, perm.sorted_token, perm.tiles, tg, tu, E, Fd, bm)
+    y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, E, D, bm)
+    torch.cuda.synchronize()
+    offs = perm.expert_offsets.tolist()
+    tok = perm.sorted_token.long()
+    with torch.no_grad():
+        for e, m in enumerate(experts):
+            a, b = offs[e], offs[e + 1]
+            assert b - a > 3000, (e, b - a)
+            xe = x2[tok[a:b]]
+            h_ref = F.linear(xe, m.up.weight) * F.silu(F.linear(xe, m.gate.weight))  # mlp.py:23
+            torch.testing.assert_close(h[a:b], h_ref, **BF16_TOL)
+            del h_ref
+            y_ref = F.linear(h[a:b], m.down.weight) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
+            torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
+            print(f"expert {e}: {b - a} rows, h and y within tolerance on every element", flush=True)
+
+
 def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
     """Tail tiles and K slices of the 256-row down kernel's last round, as the
     kernel decides them: (L, S), S = 1 when the tail runs whole (tiles of
@@ -240,7 +280,13 @@ def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_
         td = ops.expert_weight_table([ops.moe_pack_down(e.down) for e in experts], (dim, dim_ffn))
     y = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed)
     y_whole = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed, balance=False)
+    # the same calls again: which workgroup claims a tile changes from run to
+    # run, the bits may not
+    h_again = ops.moe_gemm_gate_up(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    h_gather_again = ops.moe_gemm_gate_up_gather(x, perm.sorted_token, perm.tiles, tg, tu, n_exp, dim_ffn, bm)
+    y_again = ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, n_exp, dim, bm, packed=packed)
     torch.cuda.synchronize()
+    assert torch.equal(h, h_again) and torch.equal(h, h_gather_again) and torch.equal(y, y_again)
     assert torch.equal(h, h_static) and torch.equal(h, h_gather)
     if packed:
         assert torch.equal(h, h_packed)

@@ -3,8 +3,8 @@
 (``astrai_moe_permute``), both called through the C ABI.
 
 Its outputs must equal the workspace entry point's bit for bit on every call:
-calls in a row share the library's scratch, so the second call (a smaller
-problem) and a third (another expert count) must not see stale contents.
+calls in a row share the library's scratch, so a later call (a smaller
+problem, another expert count) must not see stale contents.
 Problems too large for the scratch are refused on the host, before any device
 work (a CPU test).
 """
@@ -53,11 +53,18 @@ def _permute_noalloc(route, x, n_exp, block_m, copy_rows):
 
 @pytest.mark.gpu
 def test_noalloc_permute_matches_workspace_permute(gpu):
-    # (tokens, experts, top_k, dim, dtype, block_m, copy rows): the first uses
-    # range rows (many chunks), the second is smaller and direct, the third
-    # changes the expert count
+    # (tokens, experts, top_k, dim, dtype, block_m, copy rows). Histograms of
+    # more than 32768 counts (chunks of 32 tokens x experts) take the scan
+    # that keeps per-range expert bases in the library's scratch (ranges of 8
+    # chunks): the first case writes 157 range rows x 64 experts, the second
+    # a smaller problem over the same experts (79 rows: it must not see the
+    # first call's bases past them), the third another expert count (36 rows
+    # x 128). The last two are small enough for the scan folded into the
+    # scatter, which needs no scratch.
     cases = [
         (40000, 64, 6, 256, torch.bfloat16, 256, False),
+        (20000, 64, 6, 128, torch.bfloat16, 256, True),
+        (9000, 128, 8, 256, torch.bfloat16, 128, False),
         (3000, 64, 6, 512, torch.bfloat16, 64, True),
         (777, 8, 2, 96, torch.float32, 64, True),
     ]
