@@ -18,7 +18,10 @@
 //
 // One wave per (token, column segment); lanes stream the segment in 16-byte
 // vectors, U vectors per lane per pass with every row's loads issued before
-// the adds (more bytes in flight per wave: +15-30 % over one vector per pass).
+// the adds (more bytes in flight per wave: +15-30 % over one vector per pass;
+// at top-2, U = 8 takes a 4096-wide bf16 row in one pass: 83 -> 74 us at the
+// Mixtral shape, 5.4 TB/s, above a plain torch copy's 5.3 TB/s on the same
+// part).
 // Rows are split into segments only when there are too few tokens to keep the
 // GPU busy (decode); otherwise a wave takes the whole row. KMAX bounds top_k
 // at compile time so the row table stays in a few registers; at top-2 the
@@ -162,7 +165,7 @@ void dispatch_k(const void* y, const int32_t* token_pos, const void* row_w, cons
                 float inv_shared, int64_t n_tokens, int top_k, int64_t dim, int64_t seg_units, int64_t grid, void* out,
                 hipStream_t s) {
   if (top_k <= 2)
-    launch_combine_cfg<T, VW, 2, 2, true>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim,
+    launch_combine_cfg<T, VW, 2, 8, true>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim,
                                           seg_units, grid, out, s);
   else if (top_k <= 8)
     launch_combine_cfg<T, VW, 8, 2, false>(y, token_pos, row_w, shared, n_shared, inv_shared, n_tokens, top_k, dim,

@@ -50,8 +50,10 @@ PEAK_HBM_GBS = 8000.0
 # grouped gate/up GEMM), measured with rocprofv3 --pmc: FETCH_SIZE x 2 +
 # WRITE_SIZE (KiB, median per dispatch). A device copy in the same run reads
 # back as FETCH_SIZE = half and WRITE_SIZE = all of its bytes (FETCH_SIZE
-# counts this part's 128-byte read requests as 64 bytes), hence the 2. Sources:
-# profiles/moe_layer_*.md of each workload.
+# counts this part's 128-byte read requests as 64 bytes), hence the 2. These
+# are constants from the counter passes recorded in profiles/moe_layer_*.md
+# (TRAFFIC_SOURCE), not measured by this run: a counter pass needs the
+# profiler around the process.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
     "moe_bf16_d4096_f14336_e8_k2_t16384": (6163566.0 * 2 + 917612.9) * 1024,
     "moe_bf16_d2048_f1408_e64_k6_t8192": (779667.6 * 2 + 135168.0) * 1024,
@@ -60,6 +62,10 @@ MEASURED_TRAFFIC_BYTES: dict[str, float] = {
     "moe_bf16_d4096_f1536_e128_k8_t1024": (1685293.1 * 2 + 24585.0) * 1024,
     "moe_fp32_d512_f1024_e8_k2_t1024": (70498.3 * 2 + 8193.9) * 1024,
 }
+
+
+TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE passes of bench.py on this workload, "
+                  "profiles/moe_layer_<workload>.md (a constant from that profiled run, not measured here)")
 
 
 def _parse():
@@ -368,7 +374,23 @@ def main():
                   f"forward: {t_gu * 1e3:.4f} ms)")
     n_active = int((counts > 0).sum().item())
     weight_bytes = n_active * 3.0 * w.dim * w.dim_ffn * s
-    bytes_permute = T * w.dim * s + rows * w.dim * s + rows * 8
+    # permutation: the index outputs (routing entries and chunk histograms
+    # read; source token, weight and position of every row written) and, when
+    # the rows are copied (training, or kernels that cannot gather), x read
+    # once and written top_k times. Timed back to back from one HIP graph on
+    # the layer's own inputs (a launch of ~10-20 us is shorter than the gaps
+    # events add around it), once as the layer runs it and once copying rows.
+    n_chunks = -(-T // 32)
+    bytes_perm_index = rows * (4 + s) + 4 * w.n_experts * n_chunks + rows * (4 + s + 4)
+    bytes_perm_copy = bytes_perm_index + T * w.dim * s + rows * w.dim * s
+    perm_call = timer.last_call.get("moe_permute")
+    perm_ms = perm_copy_ms = None
+    if perm_call is not None:
+        fn_p, a_p, k_p = perm_call
+        with torch.inference_mode():
+            perm_ms, _ = back_to_back_ms(perm_call, max(stage_ms["moe_permute"], 1e-3))
+            perm_copy_ms, _ = back_to_back_ms((fn_p, a_p, {**k_p, "copy_rows": True}),
+                                              max(stage_ms["moe_permute"], 1e-3))
     bytes_combine = rows * w.dim * s + T * w.dim * s + rows * (s + 8)
     traffic = MEASURED_TRAFFIC_BYTES.get(name)
     block_m = ops.select_block_m(T, w.n_experts, w.top_k, w.dim, w.dim_ffn, w.dtype)
@@ -378,7 +400,8 @@ def main():
         gbs = gu_bytes / t_roof / 1e9
         roofline = {"kernel": "gemm_mfma_kernel<gate_up" + (", gather>" if gathered else ">"), "bound": "hbm",
                     "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
-                    "traffic": traffic, "algorithmic_bytes_per_launch": gu_bytes, "kernel_ms": t_roof * 1e3,
+                    "traffic": traffic, "traffic_source": TRAFFIC_SOURCE if traffic else None,
+                    "algorithmic_bytes_per_launch": gu_bytes, "kernel_ms": t_roof * 1e3,
                     "timing": timing}
     else:
         achieved = flops_gate_up / t_roof / 1e12
@@ -390,7 +413,8 @@ def main():
             kname = "gemm_generic_kernel<gate_up>"
         roofline = {"kernel": kname,
                     "bound": "mfma", "achieved": achieved, "peak": peak, "unit": "TFLOP/s", "frac": achieved / peak,
-                    "traffic": traffic, "algorithmic_flops_per_launch": flops_gate_up, "kernel_ms": t_roof * 1e3,
+                    "traffic": traffic, "traffic_source": TRAFFIC_SOURCE if traffic else None,
+                    "algorithmic_flops_per_launch": flops_gate_up, "kernel_ms": t_roof * 1e3,
                     "timing": timing}
 
     result = {
@@ -414,8 +438,17 @@ def main():
         "roofline": roofline,
         "kernels_ms": stage_ms,
         # with the gathering gate/up GEMM the permutation writes indices only (its rows are read by the GEMM)
-        "permute_gbs": (bytes_permute / (stage_ms["moe_permute"] / 1e3) / 1e9) if not gathered else None,
         "permute_rows": "gathered by the gate/up GEMM (no x_perm copy)" if gathered else "copied to x_perm",
+        "permute": None if perm_ms is None else {
+            "as_run_us": perm_ms * 1e3,
+            "as_run_gbs": (bytes_perm_copy if not gathered else bytes_perm_index) / (perm_ms / 1e3) / 1e9,
+            "copy_rows_us": perm_copy_ms * 1e3,
+            "copy_rows_gbs": bytes_perm_copy / (perm_copy_ms / 1e3) / 1e9,
+            "algorithmic_bytes": {"index_only": bytes_perm_index, "copy_rows": bytes_perm_copy},
+            "peak_gbs": PEAK_HBM_GBS,
+            "timing": "back-to-back launches of the layer's permute call (and the same call copying x_perm) "
+                      "replayed from one HIP graph, median of 3",
+        },
         "combine_gbs": bytes_combine / (stage_ms["moe_combine"] / 1e3) / 1e9,
         "expert_weight_stream_gbs": weight_bytes / (t_gu + t_dn) / 1e9,
         "routing": routing_stats(counts),
