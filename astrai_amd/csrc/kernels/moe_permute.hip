@@ -7,28 +7,33 @@
 // expert-major, token-ascending. Integer work only; results are bit-exact.
 //
 // Kernels:
-//   range_sum_kernel  (many chunks; see kScanDirectRows) one block per range
-//                   of kRangeChunks token chunks: the range's per-expert
-//                   counts, the column sums of its chunk histograms.
-//   scan_kernel     one block, over the ranges (or, for few chunks, over the
-//                   chunks themselves). Column sums give per-expert counts; a
+//   block_prefix_kernel  (histograms of more than kFusedScanInts counts) one
+//                   workgroup per block of kBlockRanges ranges of
+//                   kRangeChunks token chunks (or of single chunks while they
+//                   are few): each range's per-expert counts, written as the
+//                   inclusive prefix over the block's ranges, so the block's
+//                   last range holds the block's per-expert totals.
+//   scan_kernel     one workgroup, over the blocks' totals (a row per block,
+//                   n_chunks / (kRangeChunks * kBlockRanges) rows: 32 at
+//                   262144 tokens). Column sums give per-expert counts; a
 //                   block-wide exclusive scan (wave64 shuffle scan + LDS for
 //                   wave totals) gives expert offsets (the split partial sums
 //                   of each expert column are scanned by wave shuffles, not
-//                   walked by one thread); per-range bases give
-//                   every range its first slot in each expert's segment; the
-//                   GEMM row-tile list is laid out from the counts (tiles
+//                   walked by one thread); each block's base (its first slot
+//                   in each expert's segment) replaces its totals in place;
+//                   the GEMM row-tile list is laid out from the counts (tiles
 //                   never straddle experts, empty experts get none) so no
-//                   host synchronisation is needed. Splitting the column sums
-//                   off into many blocks keeps the one-block part short: it
-//                   walks n_chunks / kRangeChunks rows instead of n_chunks.
+//                   host synchronisation is needed. Before the blocks, one
+//                   workgroup walked every range (1024 rows at 262144 tokens)
+//                   and its latency grew with the token count.
 //   For histograms of at most kFusedScanInts counts (every workload of the
 //   benchmark: up to 512 chunks over 64 experts) neither runs: each scatter
 //   workgroup reads all chunk histograms itself (fused_bases) and workgroup
 //   0 writes the offsets and the tile list, one launch instead of two.
 //   scatter_kernel  grid (chunk, column split). A chunk's first slot in each
-//                   expert's segment is its range's base plus the histograms
-//                   of the earlier chunks of its range. Wave 0 ranks the chunk's
+//                   expert's segment is its block's base plus the earlier
+//                   ranges of its block (the prefix before its range) plus
+//                   the histograms of the earlier chunks of its range. Wave 0 ranks the chunk's
 //                   (token, slot) entries in order: lanes holding the same
 //                   expert are found with one ballot per expert-id bit, the
 //                   rank is the popcount of lower peer lanes, and an LDS
@@ -70,6 +75,37 @@ __global__ __launch_bounds__(256) void range_sum_kernel(
   }
 }
 
+// Ranges per block of the two-level scan, used once a scan thread would walk
+// more than kScanWalkRows ranges of its expert column.
+constexpr int kBlockRanges = 32;
+constexpr int kScanWalkRows = 32;
+
+// Memory row of scan row b when rows are blocks of `row_step` ranges: the
+// block's last range (row_step = 1: row b itself).
+__device__ __forceinline__ int64_t block_row(int64_t b, int64_t row_step, int64_t n_ranges) {
+  return min((b + 1) * row_step, n_ranges) - 1;
+}
+
+// Grid (blocks of kBlockRanges ranges, groups of 256 experts): each range's
+// counts become the inclusive prefix over its block's ranges, in place, so
+// the block's last range holds the block's per-expert totals.
+__global__ __launch_bounds__(256) void block_prefix_kernel(int32_t* __restrict__ rb, int64_t n_ranges,
+                                                           int n_experts) {
+  const int e = (int)blockIdx.y * 256 + threadIdx.x;
+  if (e >= n_experts) return;
+  const int64_t r0 = (int64_t)blockIdx.x * kBlockRanges;
+  const int64_t r1 = min(r0 + (int64_t)kBlockRanges, n_ranges);
+  int v[kBlockRanges];
+#pragma unroll
+  for (int i = 0; i < kBlockRanges; ++i) v[i] = r0 + i < r1 ? rb[(r0 + i) * n_experts + e] : 0;
+  int run = 0;
+#pragma unroll
+  for (int i = 0; i < kBlockRanges; ++i) {
+    run += v[i];
+    if (r0 + i < r1) rb[(r0 + i) * n_experts + e] = run;
+  }
+}
+
 // Inclusive scan of `v` over the block (blockDim.x == kScanThreads).
 __device__ int block_inclusive_scan(int v, int* s_wave) {
   const int lane = threadIdx.x & 63;
@@ -96,12 +132,13 @@ __device__ int block_inclusive_scan(int v, int* s_wave) {
   return r;
 }
 
-// Over `n_rows_` rows of per-expert counts (ranges or chunks): expert offsets,
-// the tile list and each row's base (expert offset + counts of the earlier
-// rows). `base` may alias `hist`: every element is read before it is written,
-// by the same thread.
+// Over `n_rows_` rows of per-expert counts: expert offsets, the tile list and
+// each row's base (expert offset + counts of the earlier rows). Row b lies at
+// memory row block_row(b, row_step, n_mem_rows) of `hist` (the totals of a
+// block of row_step ranges); `base` may alias `hist`: every element is read
+// before it is written, by the same thread.
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
-    const int32_t* hist, int64_t n_rows_, int n_experts,
+    const int32_t* hist, int64_t n_rows_, int64_t row_step, int64_t n_mem_rows, int n_experts,
     int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
     int32_t* base, int32_t* __restrict__ tiles) {
   __shared__ int s_part[kScanThreads];
@@ -125,7 +162,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   int local = 0;
   if (e < n_experts) {
 #pragma unroll 8
-    for (int64_t c = c0; c < c1; ++c) local += hist[c * n_experts + e];
+    for (int64_t c = c0; c < c1; ++c) local += hist[block_row(c, row_step, n_mem_rows) * n_experts + e];
   }
   s_part[threadIdx.x] = local;
   __syncthreads();
@@ -191,8 +228,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     int run = s_off[e] + s_part[threadIdx.x];
 #pragma unroll 8
     for (int64_t c = c0; c < c1; ++c) {
-      const int v = hist[c * n_experts + e];
-      base[c * n_experts + e] = run;
+      const int64_t m = block_row(c, row_step, n_mem_rows);
+      const int v = hist[m * n_experts + e];
+      base[m * n_experts + e] = run;
       run += v;
     }
   }
@@ -326,12 +364,12 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
 }
 
 // kFusedV > 0: the scan is folded in (fused_bases, kFusedV experts per
-// load); range_base and range_chunks are then unused.
+// load); range_base, range_chunks, n_ranges and block_ranges are then unused.
 template <typename T, bool kVec, int kFusedV = 0>
 __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
     const int32_t* __restrict__ topk_idx, const T* __restrict__ topk_w,
     const int32_t* __restrict__ chunk_hist, const int32_t* __restrict__ range_base,
-    int range_chunks, const T* __restrict__ x,
+    int range_chunks, int64_t n_ranges, int block_ranges, const T* __restrict__ x,
     int64_t n_tokens, int n_experts, int top_k, int64_t dim,
     int32_t* __restrict__ sorted_token, T* __restrict__ sorted_w,
     int32_t* __restrict__ token_pos, T* __restrict__ x_perm,
@@ -367,10 +405,16 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
                          tiles, cnt, s_tot, s_wave);
   } else {
     // the chunk's first slot per expert: its range's base plus the earlier
-    // chunks of the range
+    // chunks of the range. With blocks of ranges (block_ranges > 0) the
+    // range's base is its block's base (held in the block's last range) plus
+    // the earlier ranges of its block (the inclusive prefix of the range
+    // before it).
     const int64_t r = chunk / range_chunks;
+    const int64_t blk0 = block_ranges > 0 ? r / block_ranges * block_ranges : r;
+    const int64_t brow = block_ranges > 0 ? block_row(r / block_ranges, block_ranges, n_ranges) : r;
     for (int e = threadIdx.x; e < n_experts; e += kScatterThreads) {
-      int b = range_base[r * n_experts + e];
+      int b = range_base[brow * n_experts + e];
+      if (r > blk0) b += range_base[(r - 1) * n_experts + e];
       for (int64_t c = r * range_chunks; c < chunk; ++c) b += chunk_hist[c * n_experts + e];
       cnt[e] = b;
     }
@@ -497,11 +541,13 @@ int64_t permute_scratch_ints(int64_t n_tokens, int n_experts) {
 
 template <typename T, bool kVec, int kFusedV>
 void launch_scatter(dim3 grid, hipStream_t s, const int32_t* topk_idx, const void* topk_w, const int32_t* chunk_hist,
-                    const int32_t* range_base, int range_chunks, const void* x, int64_t n_tokens, int n_experts,
+                    const int32_t* range_base, int range_chunks, int64_t n_ranges, int block_ranges, const void* x,
+                    int64_t n_tokens, int n_experts,
                     int top_k, int64_t dim, int32_t* sorted_token, void* sorted_w, int32_t* token_pos, void* x_perm,
                     int block_m, int64_t tile_capacity, int32_t* expert_offsets, int32_t* tiles) {
   hipLaunchKernelGGL((scatter_kernel<T, kVec, kFusedV>), grid, dim3(kScatterThreads), 0, s, topk_idx,
-                     static_cast<const T*>(topk_w), chunk_hist, range_base, range_chunks, static_cast<const T*>(x),
+                     static_cast<const T*>(topk_w), chunk_hist, range_base, range_chunks, n_ranges, block_ranges,
+                     static_cast<const T*>(x),
                      n_tokens, n_experts, top_k, dim, sorted_token, static_cast<T*>(sorted_w), token_pos,
                      static_cast<T*>(x_perm), block_m, tile_capacity, expert_offsets, tiles);
 }
@@ -521,16 +567,28 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
   const int64_t n_ranges = ceil_div(nc, range_chunks);
   int32_t* range_base = chunk_base;  // n_ranges * n_experts <= n_chunks * n_experts
   int rc = ASTRAI_MOE_OK;
+  int block_ranges = 0;
   if (!fused) {
     if (range_chunks > 1) {
       hipLaunchKernelGGL(range_sum_kernel, dim3((unsigned)n_ranges), dim3(256), 0, s,
                          chunk_hist, nc, n_experts, range_base);
       if ((rc = check_launch("range_sum_kernel"))) return rc;
     }
+    // two levels once a scan thread would walk more than kScanWalkRows rows
+    int ep = 1;
+    while (ep < n_experts) ep *= 2;
+    int64_t scan_rows = n_ranges, row_step = 1;
+    if (range_chunks > 1 && ceil_div(n_ranges, std::max(1, kScanThreads / ep)) > kScanWalkRows) {
+      block_ranges = kBlockRanges;
+      scan_rows = ceil_div(n_ranges, (int64_t)kBlockRanges);
+      row_step = kBlockRanges;
+      hipLaunchKernelGGL(block_prefix_kernel, dim3((unsigned)scan_rows, (unsigned)ceil_div(n_experts, 256)),
+                         dim3(256), 0, s, range_base, n_ranges, n_experts);
+      if ((rc = check_launch("block_prefix_kernel"))) return rc;
+    }
     hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s,
-                       range_chunks > 1 ? range_base : chunk_hist, n_ranges,
-                       n_experts, block_m, tile_capacity, expert_offsets,
-                       range_base, tiles);
+                       range_chunks > 1 || block_ranges > 0 ? range_base : chunk_hist, scan_rows, row_step,
+                       n_ranges, n_experts, block_m, tile_capacity, expert_offsets, range_base, tiles);
     rc = check_launch("scan_kernel");
     if (rc || nc == 0) return rc;
   }
@@ -547,7 +605,8 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
   // the fused scan reads 16-byte vectors of 4 experts where rows allow it
   const bool v4 = n_experts % 4 == 0 && reinterpret_cast<uintptr_t>(chunk_hist) % 16 == 0;
 #define ASTRAI_SCATTER(VEC, FV)                                                                                       \
-  launch_scatter<T, VEC, FV>(grid, s, topk_idx, topk_w, chunk_hist, range_base, range_chunks, x, n_tokens, n_experts, \
+  launch_scatter<T, VEC, FV>(grid, s, topk_idx, topk_w, chunk_hist, range_base, range_chunks, n_ranges,            \
+                             block_ranges, x, n_tokens, n_experts,                                                   \
                              top_k, dim, sorted_token, sorted_w, token_pos, x_perm, block_m, tile_capacity,          \
                              expert_offsets, tiles)
   if (!fused) {

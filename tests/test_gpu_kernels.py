@@ -95,8 +95,10 @@ PERM_CASES = [
     (2048, 128, 8, 512, 32),
     (1000, 3, 2, 40, 64),
     (500, 1024, 4, 64, 32),
-    (262144, 64, 6, 64, 256),  # 1.57 M rows, many chunks in the scan
+    (262144, 64, 6, 64, 256),  # 1.57 M rows: ranges scanned in blocks (two-level scan)
     (100003, 32, 4, 72, 32),  # ragged last chunk; rows copied element-wise (72 x 2 bytes is not 16-byte aligned)
+    (262144, 1024, 8, 16, 256),  # two-level scan over 4 groups of 256 expert columns
+    (8448, 1024, 2, 16, 64),  # 33 ranges: a last block holding a single range
 ]
 
 
