@@ -474,14 +474,14 @@ __device__ __forceinline__ void bwd_epilogue_any(f32x4_t (&acc)[BwdCfg::WM / 16]
 // and runs the tile's epilogue. The walk is recomputed from the same tile
 // list and the GEMM launch's grid, so both kernels agree on the split.
 template <Bwd kMode>
-__global__ __launch_bounds__(512) void bwd_split_reduce_kernel(const BwdArgs p) {
+__global__ __launch_bounds__(64) void bwd_split_reduce_kernel(const BwdArgs p) {
   static_assert(kMode == Bwd::kDgradIn || kMode == Bwd::kDgradInAdd, "only dgrad_in splits its tail");
   const RowTileWalk<true> walk(p, true);
   const int u = blockIdx.x;
   if (walk.w.S < 2 || u >= walk.w.total - walk.w.full) return;
   TileInfo t;
   walk.seek(walk.w.full + u * walk.w.S, t);  // the tile's first slice
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = blockIdx.y, lane = threadIdx.x;  // one wave per (tile, matrix-core wave)
   constexpr int MT16 = BwdCfg::WM / 16, NT16 = BwdCfg::WN / 16;
   constexpr int kUnitVecs = kSplitUnitFloats / 4;
   const f32x4_t* pp = reinterpret_cast<const f32x4_t*>(p.part) + (int64_t)u * walk.w.S * kUnitVecs +
@@ -746,7 +746,8 @@ int launch_bwd(BwdArgs p, int64_t total, hipStream_t s, const char* name, const 
     if (p.part == nullptr) return ASTRAI_MOE_OK;
     hipLaunchKernelGGL((gemm_bwd_kernel<kMode, true>), dim3((unsigned)grid), dim3(BwdCfg::THREADS), 0, s, p);
     if (int rc = check_launch(name)) return rc;
-    hipLaunchKernelGGL((bwd_split_reduce_kernel<kMode>), dim3((unsigned)((grid + 1) / 2)), dim3(512), 0, s, p);
+    hipLaunchKernelGGL((bwd_split_reduce_kernel<kMode>), dim3((unsigned)((grid + 1) / 2), BwdCfg::MW), dim3(64), 0, s,
+                       p);
     return check_launch("bwd_split_reduce_kernel");
   }
   return ASTRAI_MOE_OK;

@@ -684,13 +684,15 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
   }
 }
 
-// The epilogue of the split tail tiles (SplitWalk): workgroup t sums the S
-// partials of tail tile t in slice order, wave w taking the accumulators of
-// matrix-core wave w, and stores them as the streaming kernel stores a whole
-// tile. G is the streaming launch's grid; the walk is recomputed from the
+// The epilogue of the split tail tiles (SplitWalk): workgroup (t, w), one
+// wave, sums the S partials of matrix-core wave w's accumulators of tail
+// tile t in slice order and stores them as that wave stores a whole tile.
+// (One wave per workgroup: with a workgroup of 8 waves per tile, the 32-64
+// tail tiles of the Mixtral-shaped down GEMM left most compute units idle
+// and the reduce took ~45 us.) G is the streaming launch's grid; the walk is recomputed from the
 // same tile list, so both kernels agree on which tiles were split.
 template <bool kGateUp, bool kSave>
-__global__ __launch_bounds__(512) void split_reduce_kernel(const float* __restrict__ part,
+__global__ __launch_bounds__(64) void split_reduce_kernel(const float* __restrict__ part,
                                                            const int32_t* __restrict__ tiles, int capacity,
                                                            int n_tiles_n, int K, int G,
                                                            const bf16_t* __restrict__ row_w, bf16_t* __restrict__ C,
@@ -704,7 +706,7 @@ __global__ __launch_bounds__(512) void split_reduce_kernel(const float* __restri
   const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
   const int t_row0 = ti[1];
   const int t_rows = min(Cfg::BM, ti[2] - t_row0);
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = blockIdx.y, lane = threadIdx.x;
   constexpr int MT16 = Cfg::WM / 16, NT16 = Cfg::WN / 16;
   constexpr int kUnitVecs = kSplitUnitFloats / 4;
   const f32x4_t* p = reinterpret_cast<const f32x4_t*>(part) + (int64_t)t * walk.S * kUnitVecs +
@@ -969,7 +971,7 @@ int launch_stream(const void* A, const int32_t* tiles, int64_t capacity, const v
   if (part == nullptr) return ASTRAI_MOE_OK;
   // whether the tail was split is decided on the device (the live tile count
   // is there): at most G / 2 tail tiles, one workgroup each
-  hipLaunchKernelGGL((split_reduce_kernel<kGateUp, kSave>), dim3((unsigned)((grid + 1) / 2)), dim3(512), 0, s,
+  hipLaunchKernelGGL((split_reduce_kernel<kGateUp, kSave>), dim3((unsigned)((grid + 1) / 2), Cfg::MW), dim3(64), 0, s,
                      part, tiles, (int)capacity, (int)n_tiles_n, (int)K, (int)grid,
                      static_cast<const bf16_t*>(row_w), static_cast<bf16_t*>(C), (int)N, static_cast<bf16_t*>(S0));
   return check_launch("split_reduce_kernel");
