@@ -18,6 +18,10 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;             // K elements per stage
+// K steps per tile below which the 256-row kernels let the matrix-core waves
+// whose rows are all padding (an expert's last tile of at most 128 rows) skip
+// their MFMAs and stores
+constexpr int kIdleMaxSteps = 48;
 constexpr int kRowBytes = kBK * 2;  // 128 bytes per staged row
 constexpr int kXcds = 8;
 

@@ -619,19 +619,27 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
   for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
   int mt = 0, nt = 0, k0 = 0, k1 = 0, unit = -1;
   bool claiming = wave == 0;  // matrix-core wave 0 makes the run-time claims
+  // first row of this wave's half where padding-only waves idle (short
+  // tiles), else -1: no tile has that few rows, so no wave idles. Wave 0
+  // (rows from 0, every tile has at least one) never idles, so the run-time
+  // claims it makes always happen.
+  const int idle_row0 = __builtin_amdgcn_readfirstlane(KT < kIdleMaxSteps ? wm * Cfg::WM : -1);
   walk.item(seq.id(0), mt, nt, k0, k1, unit);
   for (int idx = 0;; ++idx) {
     const int claim_at = (claiming && seq.claims_next(idx)) ? k1 - kClaimLead : -1;
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int t_row0 = ti[1];
     const int t_rows = min(Cfg::BM, ti[2] - t_row0);
-    // An expert's last tile with at most BM / 2 rows: the waves of the
-    // second half hold only padding rows, so they keep the step barriers and
-    // the next item's prefetch but issue no MFMAs and store nothing. (Measured
-    // in one process, builds alternating, bit-identical: fine-grained down
-    // GEMM +6.7 %, Zipf-skewed gate/up +6.3 %, Mixtral shape within +-0.4 %,
-    // where such tiles wait on their data more than on the matrix cores.)
-    const bool idle = wm * Cfg::WM >= t_rows;
+    // An expert's last tile with at most BM / 2 rows, in GEMMs of short tiles
+    // (fewer than kIdleMaxSteps K steps): the waves of the second half hold
+    // only padding rows, so they keep the step barriers and the next item's
+    // prefetch but issue no MFMAs and store nothing. Measured in one process,
+    // builds alternating, bit-identical: fine-grained down GEMM +6.7 %,
+    // Zipf-skewed gate/up +6.3 %. With long tiles (Mixtral shape) it was
+    // within +-0.4 %, and the workgroups of such tiles ran ahead of the others
+    // of their XCD, which then shared fewer operand strips in L2 (gate/up
+    // FETCH_SIZE +46 %, hits 78 -> 68 %).
+    const bool idle = idle_row0 >= t_rows;
 #pragma unroll
     for (int i = 0; i < MT16; ++i)
 #pragma unroll
