@@ -55,12 +55,12 @@ PEAK_HBM_GBS = 8000.0
 # (TRAFFIC_SOURCE), not measured by this run: a counter pass needs the
 # profiler around the process.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
-    "moe_bf16_d4096_f14336_e8_k2_t16384": (6163566.0 * 2 + 917612.9) * 1024,
-    "moe_bf16_d2048_f1408_e64_k6_t8192": (779667.6 * 2 + 135168.0) * 1024,
-    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (760961.2 * 2 + 135168.1) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t64": (1567802.7 * 2 + 1538.2) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t1024": (1685293.1 * 2 + 24585.0) * 1024,
-    "moe_fp32_d512_f1024_e8_k2_t1024": (70498.3 * 2 + 8193.9) * 1024,
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (6385666.2 * 2 + 917612.8) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192": (1216830.4 * 2 + 135169.4) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (1083143.8 * 2 + 135168.7) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t64": (1542816.2 * 2 + 1537.4) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t1024": (1681673.8 * 2 + 24585.0) * 1024,
+    "moe_fp32_d512_f1024_e8_k2_t1024": (73295.3 * 2 + 8195.2) * 1024,
 }
 
 
