@@ -18,10 +18,17 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBK = 64;             // K elements per stage
-// K steps per tile below which the 256-row kernels let the matrix-core waves
-// whose rows are all padding (an expert's last tile of at most 128 rows) skip
-// their MFMAs and stores
-constexpr int kIdleMaxSteps = 48;
+
+// Padding-only waves: a matrix-core wave whose first row is wave_row0 idles
+// on a tile of `rows` valid rows iff idle_threshold(eligible, wave_row0) >=
+// rows. A tile that may not idle gets -1, which no row count reaches (every
+// tile has at least one row), and wave 0 (rows from 0) never idles, so the
+// run-time claims it makes always happen.
+__host__ __device__ constexpr int idle_threshold(bool eligible, int wave_row0) { return eligible ? wave_row0 : -1; }
+static_assert(!(idle_threshold(false, 128) >= 1), "a tile that may not idle keeps every wave");
+static_assert(!(idle_threshold(true, 0) >= 1), "wave 0 never idles");
+static_assert(idle_threshold(true, 128) >= 128 && !(idle_threshold(true, 128) >= 129),
+              "the second half idles exactly on tiles of at most 128 rows");
 constexpr int kRowBytes = kBK * 2;  // 128 bytes per staged row
 constexpr int kXcds = 8;
 

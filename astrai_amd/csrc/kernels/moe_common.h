@@ -91,6 +91,21 @@ inline int64_t n_chunks(int64_t n_tokens) {
   return ceil_div(n_tokens, ASTRAI_MOE_CHUNK_TOKENS);
 }
 
+// Row tiles per group of the GEMMs' tile walk (the 32 workgroups of one XCD
+// take a group's row tiles for a run of column tiles).
+constexpr int kTileGroup = 8;
+// K steps (of 64) per tile below which the 256-row GEMM kernels let the
+// matrix-core waves whose rows are all padding (an expert's last tile of at
+// most 128 rows) skip their MFMAs and stores on every tile; with longer tiles
+// only in the tail of the tile list (tiles[3] on).
+constexpr int kIdleMaxSteps = 48;
+// Rows of at least this many elements (gate/up tiles of kIdleMaxSteps K
+// steps or more): the permutation writes each expert's whole groups of
+// kTileGroup tiles first, so that a group of the walk holds one expert's
+// tiles, and the rest as the list's tail. Narrower rows keep expert order
+// (with short tiles the grouped order measured slower on a skewed router).
+constexpr int64_t kGroupTilesMinDim = 64 * kIdleMaxSteps;
+
 }  // namespace astrai_moe
 
 #define ASTRAI_REQUIRE(cond, ...)                                  \

@@ -635,15 +635,17 @@ __global__ __launch_bounds__(Cfg::THREADS, 1) void gemm_bwd_kernel(const BwdArgs
 #pragma unroll
   for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
   constexpr bool kIdleHalf = kMode == Bwd::kDgradDown;
+  // first row tile where padding-only waves idle: every tile with short
+  // tiles, else the tiles after the list's whole groups (as in the forward)
+  const int idle_mt0 = kIdleHalf ? __builtin_amdgcn_readfirstlane(p.K / kBK < kIdleMaxSteps ? 0 : p.tiles[3]) : 0;
   while (true) {
-    // dgrad_down with short tiles (fewer than kIdleMaxSteps K steps): in an
-    // expert's last row tile of at most BM / 2 rows the waves of the second
-    // half hold only padding rows; they keep the step barriers and the next
-    // tile's prefetch but issue no MFMAs and store nothing, as in the forward
-    // kernel (bit-identical; fine-grained shape +1.9 %). In the dgrad_in pair
-    // it measured within +-1.6 %, and dgrad_in_add's K loop then spilled a
-    // fragment.
-    if (kIdleHalf && t.ksteps < kIdleMaxSteps && wm * Cfg::WM >= t.rows) {
+    // dgrad_down: in an expert's last row tile of at most BM / 2 rows the
+    // waves of the second half hold only padding rows; they keep the step
+    // barriers and the next tile's prefetch but issue no MFMAs and store
+    // nothing, as in the forward kernel (bit-identical; fine-grained shape
+    // +1.9 %). In the dgrad_in pair it measured within +-1.6 %, and
+    // dgrad_in_add's K loop then spilled a fragment.
+    if (kIdleHalf && idle_threshold(t.mt >= idle_mt0, wm * Cfg::WM) >= t.rows) {
       for (int kt = kSplit ? t.k0 : 0; kt < t.ksteps; ++kt) {
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();  // X_g

@@ -259,6 +259,7 @@ struct StreamCfg {
   // GEMMs +0.1 / +0.5 % (Mixtral shape) and +1.1 / +4.8 % (fine-grained),
   // gate/up -2.7 % and -8.7 % (its activation strips then serve 4 XCDs).
   static constexpr int BM = 256, BN = 256, GM = kGateUp ? 8 : 16;
+  static_assert(GM % kTileGroup == 0, "walk groups hold whole groups of the tile list");
   static constexpr int WGM = 2, WGN = 4, MW = 8, DW = 4;  // matrix-core waves (WGM x WGN), DMA waves
   static constexpr int WAVES = MW + DW, THREADS = WAVES * 64;
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // 128 x 64 per matrix-core wave
@@ -619,27 +620,31 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
   for (int r = 0; r < PD; ++r) fa[r % AR] = rdA(vA, 0, r);
   int mt = 0, nt = 0, k0 = 0, k1 = 0, unit = -1;
   bool claiming = wave == 0;  // matrix-core wave 0 makes the run-time claims
-  // first row of this wave's half where padding-only waves idle (short
-  // tiles), else -1: no tile has that few rows, so no wave idles. Wave 0
-  // (rows from 0, every tile has at least one) never idles, so the run-time
-  // claims it makes always happen.
-  const int idle_row0 = __builtin_amdgcn_readfirstlane(KT < kIdleMaxSteps ? wm * Cfg::WM : -1);
+  // first row of this wave's half: a tile with no more rows leaves the wave
+  // only padding (idle_threshold). idle_mt0: the first
+  // row tile where such waves idle: every tile in GEMMs of short tiles (fewer
+  // than kIdleMaxSteps K steps), else the tiles after the list's whole groups
+  // of one expert (tiles[3]), which the walk reaches last.
+  const int idle_row0 = __builtin_amdgcn_readfirstlane(wm * Cfg::WM);
+  const int idle_mt0 = __builtin_amdgcn_readfirstlane(KT < kIdleMaxSteps ? 0 : tiles[3]);
   walk.item(seq.id(0), mt, nt, k0, k1, unit);
   for (int idx = 0;; ++idx) {
     const int claim_at = (claiming && seq.claims_next(idx)) ? k1 - kClaimLead : -1;
     const int32_t* ti = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)mt * ASTRAI_MOE_TILE_STRIDE;
     const int t_row0 = ti[1];
     const int t_rows = min(Cfg::BM, ti[2] - t_row0);
-    // An expert's last tile with at most BM / 2 rows, in GEMMs of short tiles
-    // (fewer than kIdleMaxSteps K steps): the waves of the second half hold
-    // only padding rows, so they keep the step barriers and the next item's
-    // prefetch but issue no MFMAs and store nothing. Measured in one process,
-    // builds alternating, bit-identical: fine-grained down GEMM +6.7 %,
-    // Zipf-skewed gate/up +6.3 %. With long tiles (Mixtral shape) it was
-    // within +-0.4 %, and the workgroups of such tiles ran ahead of the others
-    // of their XCD, which then shared fewer operand strips in L2 (gate/up
-    // FETCH_SIZE +46 %, hits 78 -> 68 %).
-    const bool idle = idle_row0 >= t_rows;
+    // An expert's last tile with at most BM / 2 rows: the waves of the second
+    // half hold only padding rows, so they keep the step barriers and the
+    // next item's prefetch but issue no MFMAs and store nothing. Measured in
+    // one process, builds alternating, bit-identical: fine-grained down GEMM
+    // +6.7 %, Zipf-skewed gate/up +6.3 %. With long tiles (Mixtral shape)
+    // inside the whole groups it was within +-0.4 %, and the workgroups of
+    // such tiles ran ahead of the others of their XCD, which then shared
+    // fewer operand strips in L2 (gate/up FETCH_SIZE +46 %, hits 78 -> 68 %):
+    // long tiles idle only after the whole groups.
+    // (as a row threshold: the two compares joined by && made the compiler
+    // spill the prefetched fragments around the branch)
+    const bool idle = idle_threshold(mt >= idle_mt0, idle_row0) >= t_rows;
 #pragma unroll
     for (int i = 0; i < MT16; ++i)
 #pragma unroll

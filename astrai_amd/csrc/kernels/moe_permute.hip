@@ -7,33 +7,38 @@
 // expert-major, token-ascending. Integer work only; results are bit-exact.
 //
 // Kernels:
-//   block_prefix_kernel  (histograms of more than kFusedScanInts counts) one
-//                   workgroup per block of kBlockRanges ranges of
-//                   kRangeChunks token chunks (or of single chunks while they
-//                   are few): each range's per-expert counts, written as the
-//                   inclusive prefix over the block's ranges, so the block's
-//                   last range holds the block's per-expert totals.
-//   scan_kernel     one workgroup, over the blocks' totals (a row per block,
-//                   n_chunks / (kRangeChunks * kBlockRanges) rows: 32 at
-//                   262144 tokens). Column sums give per-expert counts; a
-//                   block-wide exclusive scan (wave64 shuffle scan + LDS for
-//                   wave totals) gives expert offsets (the split partial sums
-//                   of each expert column are scanned by wave shuffles, not
-//                   walked by one thread); each block's base (its first slot
-//                   in each expert's segment) replaces its totals in place;
-//                   the GEMM row-tile list is laid out from the counts (tiles
-//                   never straddle experts, empty experts get none) so no
-//                   host synchronisation is needed. Before the blocks, one
-//                   workgroup walked every range (1024 rows at 262144 tokens)
-//                   and its latency grew with the token count.
+//   range_sum_kernel     (histograms of more than kFusedScanInts counts, and
+//                   more than kScanDirectRows chunks per scan thread) one
+//                   workgroup per range of kRangeChunks token chunks: the
+//                   range's per-expert counts.
+//   block_prefix_kernel  (once a scan thread would walk more than
+//                   kScanWalkRows ranges) grid (blocks of kBlockRanges
+//                   ranges, groups of 256 experts): each range's counts become
+//                   the inclusive prefix over its block, in place, so the
+//                   block's last range holds the block's per-expert totals.
+//   scan_kernel     one workgroup over the rows left (chunks, ranges or
+//                   blocks: at most 32 rows per thread of an expert column;
+//                   32 blocks at 262144 tokens and 1024 experts). Column sums
+//                   give per-expert counts; a block-wide exclusive scan
+//                   (wave64 shuffle scan + LDS for wave totals) gives expert
+//                   offsets (the split partial sums of each expert column are
+//                   scanned by wave shuffles, not walked by one thread); each
+//                   row's base (its first slot in each expert's segment)
+//                   replaces its counts in place; the GEMM row-tile list is
+//                   laid out from the counts (tiles never straddle experts,
+//                   empty experts get none; for rows of at least
+//                   kGroupTilesMinDim elements each expert's whole groups of
+//                   kTileGroup tiles come first and the rest after them) so
+//                   no host synchronisation is needed.
 //   For histograms of at most kFusedScanInts counts (every workload of the
-//   benchmark: up to 512 chunks over 64 experts) neither runs: each scatter
+//   benchmark: up to 512 chunks over 64 experts) none of these runs: each scatter
 //   workgroup reads all chunk histograms itself (fused_bases) and workgroup
 //   0 writes the offsets and the tile list, one launch instead of two.
 //   scatter_kernel  grid (chunk, column split). A chunk's first slot in each
-//                   expert's segment is its block's base plus the earlier
-//                   ranges of its block (the prefix before its range) plus
-//                   the histograms of the earlier chunks of its range. Wave 0 ranks the chunk's
+//                   expert's segment is its row's base; in block mode, its
+//                   block's base plus the earlier ranges of its block (the
+//                   prefix before its range); plus the histograms of the
+//                   earlier chunks of its range. Wave 0 ranks the chunk's
 //                   (token, slot) entries in order: lanes holding the same
 //                   expert are found with one ballot per expert-id bit, the
 //                   rank is the popcount of lower peer lanes, and an LDS
@@ -86,6 +91,22 @@ __device__ __forceinline__ int64_t block_row(int64_t b, int64_t row_step, int64_
   return min((b + 1) * row_step, n_ranges) - 1;
 }
 
+// Tiles of an expert with `ntile` tiles that go to the grouped head of the
+// tile list: its whole groups of kTileGroup when grouping, else none (the
+// list is then in expert order). The GEMMs walk row tiles in groups of
+// kTileGroup (so that the 32 workgroups of one XCD share operand strips in
+// L2), and a group that straddles two experts needs both experts' weight
+// strips.
+__device__ __forceinline__ int grouped_tiles(int ntile, bool group) {
+  return group ? ntile - ntile % kTileGroup : 0;
+}
+// Position of tile j of an expert: the grouped head (pure0: the expert's
+// first tile there, the exclusive prefix of grouped tiles) or the tail
+// (left0: its first tile there), each in expert order.
+__device__ __forceinline__ int64_t tile_slot(int j, int npure, int64_t pure0, int64_t left0) {
+  return j < npure ? pure0 + j : left0 + (j - npure);
+}
+
 // Grid (blocks of kBlockRanges ranges, groups of 256 experts): each range's
 // counts become the inclusive prefix over its block's ranges, in place, so
 // the block's last range holds the block's per-expert totals.
@@ -136,10 +157,12 @@ __device__ int block_inclusive_scan(int v, int* s_wave) {
 // each row's base (expert offset + counts of the earlier rows). Row b lies at
 // memory row block_row(b, row_step, n_mem_rows) of `hist` (the totals of a
 // block of row_step ranges); `base` may alias `hist`: every element is read
-// before it is written, by the same thread.
+// before it is written, by the same thread. kBlocks = false: row_step is 1
+// and row b is memory row b (no per-row index arithmetic).
+template <bool kBlocks>
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const int32_t* hist, int64_t n_rows_, int64_t row_step, int64_t n_mem_rows, int n_experts,
-    int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
+    int block_m, int64_t tile_capacity, bool group, int32_t* __restrict__ expert_offsets,
     int32_t* base, int32_t* __restrict__ tiles) {
   __shared__ int s_part[kScanThreads];
   __shared__ int s_wave[kScanThreads / 64];
@@ -162,7 +185,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   int local = 0;
   if (e < n_experts) {
 #pragma unroll 8
-    for (int64_t c = c0; c < c1; ++c) local += hist[block_row(c, row_step, n_mem_rows) * n_experts + e];
+    for (int64_t c = c0; c < c1; ++c) local += hist[(kBlocks ? block_row(c, row_step, n_mem_rows) : c) * n_experts + e];
   }
   s_part[threadIdx.x] = local;
   __syncthreads();
@@ -196,14 +219,23 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   }
   __syncthreads();
 
-  // Expert offsets and tile starts: block scans over expert ids.
+  // Expert offsets and tile starts: block scans over expert ids (rows,
+  // tiles, tiles in whole groups; the last expert's thread publishes the
+  // whole-group total, where the leftover tiles start).
   const int cnt = (threadIdx.x < n_experts) ? s_cnt[threadIdx.x] : 0;
   const int ntile = (cnt + block_m - 1) / block_m;
+  const int npure = grouped_tiles(ntile, group);
   const int cnt_incl = block_inclusive_scan(cnt, s_wave);
   const int tile_incl = block_inclusive_scan(ntile, s_wave);
+  const int pure_incl = block_inclusive_scan(npure, s_wave);
+  __shared__ int s_npure;
+  if (threadIdx.x == n_experts - 1) s_npure = pure_incl;
+  __syncthreads();
+  const int n_pure = s_npure;
   if (threadIdx.x < n_experts) {
     const int off = cnt_incl - cnt;
-    const int tile0 = tile_incl - ntile;
+    const int tile0 = tile_incl - ntile, pure0 = pure_incl - npure;
+    const int64_t left0 = (int64_t)n_pure + (tile0 - pure0);
     s_off[threadIdx.x] = off;
     expert_offsets[threadIdx.x] = off;
     if (threadIdx.x == n_experts - 1) {
@@ -211,11 +243,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       tiles[0] = tile_incl;
       tiles[1] = block_m;
       tiles[2] = (int32_t)tile_capacity;
-      tiles[3] = 0;
+      tiles[3] = group ? n_pure : tile_incl;
     }
     // the expert's row tiles (stores only: nothing waits on them)
-    for (int j = 0; j < ntile && tile0 + j < tile_capacity; ++j) {
-      int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)(tile0 + j) * ASTRAI_MOE_TILE_STRIDE;
+    for (int j = 0; j < ntile; ++j) {
+      const int64_t slot = tile_slot(j, npure, pure0, left0);
+      if (slot >= tile_capacity) continue;
+      int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER + slot * ASTRAI_MOE_TILE_STRIDE;
       t[0] = threadIdx.x;
       t[1] = off + j * block_m;
       t[2] = off + cnt;
@@ -228,7 +262,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     int run = s_off[e] + s_part[threadIdx.x];
 #pragma unroll 8
     for (int64_t c = c0; c < c1; ++c) {
-      const int64_t m = block_row(c, row_step, n_mem_rows);
+      const int64_t m = kBlocks ? block_row(c, row_step, n_mem_rows) : c;
       const int v = hist[m * n_experts + e];
       base[m * n_experts + e] = run;
       run += v;
@@ -236,32 +270,44 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   }
 }
 
-// Exclusive prefix sums over the block (blockDim.x == kScatterThreads) of two
+// Exclusive prefix sums over the block (blockDim.x == kScatterThreads) of N
 // values per thread at once (each thread holding the sums of its own run),
-// and their block totals.
-__device__ void scatter_block_exclusive_scan2(int& a, int& b, int* s_wave, int& total_a, int& total_b) {
+// and their block totals. s_wave holds N * kScatterThreads / 64 ints.
+template <int N>
+__device__ void scatter_block_exclusive_scan(int (&v)[N], int* s_wave, int (&total)[N]) {
+  constexpr int kW = kScatterThreads / 64;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  int ia = a, ib = b;
+  int inc[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) inc[i] = v[i];
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int oa = __shfl_up(ia, off, 64);
-    const int ob = __shfl_up(ib, off, 64);
-    if (lane >= off) ia += oa, ib += ob;
-  }
-  if (lane == 63) s_wave[wave] = ia, s_wave[kScatterThreads / 64 + wave] = ib;
-  __syncthreads();
-  int before_a = 0, before_b = 0;
-  total_a = total_b = 0;
 #pragma unroll
-  for (int w = 0; w < kScatterThreads / 64; ++w) {
-    const int ta = s_wave[w], tb = s_wave[kScatterThreads / 64 + w];
-    if (w < wave) before_a += ta, before_b += tb;
-    total_a += ta, total_b += tb;
+    for (int i = 0; i < N; ++i) {
+      const int o = __shfl_up(inc[i], off, 64);
+      if (lane >= off) inc[i] += o;
+    }
   }
-  a = before_a + ia - a;
-  b = before_b + ib - b;
+  if (lane == 63) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) s_wave[i * kW + wave] = inc[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    int before = 0;
+    total[i] = 0;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      const int t = s_wave[i * kW + w];
+      if (w < wave) before += t;
+      total[i] += t;
+    }
+    v[i] = before + inc[i] - v[i];
+  }
 }
+
 
 // The scan folded into the scatter, for histograms of at most
 // kFusedScanInts counts: every workgroup reads all chunk histograms, V
@@ -275,7 +321,7 @@ constexpr int kFusedScanInts = 32768;
 
 template <int V>
 __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, int n_experts, int64_t chunk,
-                            int block_m, int64_t tile_capacity, int32_t* __restrict__ expert_offsets,
+                            int block_m, int64_t tile_capacity, bool group, int32_t* __restrict__ expert_offsets,
                             int32_t* __restrict__ tiles, int* cnt, int* s_tot, int* s_wave) {
   const int t = threadIdx.x;
   const int cw = n_experts / V;  // V divides n_experts
@@ -328,12 +374,18 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
     run += tot4[j];
   }
   const bool write_list = blockIdx.x == 0 && blockIdx.y == 0;
-  int ntile_run = 0;
+  int ntile_run = 0, pure_run = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ntile_run += (tot4[j] + block_m - 1) / block_m;
-  int n_rows = 0, n_tiles = 0;
-  int off = run, tile0 = ntile_run;
-  scatter_block_exclusive_scan2(off, tile0, s_wave, n_rows, n_tiles);
+  for (int j = 0; j < 4; ++j) {
+    const int nt = (tot4[j] + block_m - 1) / block_m;
+    ntile_run += nt;
+    pure_run += grouped_tiles(nt, group);
+  }
+  // exclusive prefixes over experts of rows, tiles and whole-group tiles
+  int pre[3] = {run, ntile_run, pure_run}, tot[3];
+  scatter_block_exclusive_scan<3>(pre, s_wave, tot);
+  int off = pre[0], tile0 = pre[1], pure0 = pre[2];
+  const int n_rows = tot[0], n_tiles = tot[1], n_pure = tot[2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = 4 * t + j;
@@ -342,13 +394,18 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
       if (write_list) {
         expert_offsets[e] = off;
         const int ntile = (tot4[j] + block_m - 1) / block_m;
-        for (int k = 0; k < ntile && tile0 + k < tile_capacity; ++k) {
-          int32_t* tt = tiles + ASTRAI_MOE_TILE_HEADER + (int64_t)(tile0 + k) * ASTRAI_MOE_TILE_STRIDE;
+        const int npure = grouped_tiles(ntile, group);
+        const int64_t left0 = (int64_t)n_pure + (tile0 - pure0);
+        for (int k = 0; k < ntile; ++k) {
+          const int64_t slot = tile_slot(k, npure, pure0, left0);
+          if (slot >= tile_capacity) continue;
+          int32_t* tt = tiles + ASTRAI_MOE_TILE_HEADER + slot * ASTRAI_MOE_TILE_STRIDE;
           tt[0] = e;
           tt[1] = off + k * block_m;
           tt[2] = off + tot4[j];
         }
         tile0 += ntile;
+        pure0 += npure;
       }
       off += tot4[j];
     }
@@ -358,7 +415,7 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
     tiles[0] = n_tiles;
     tiles[1] = block_m;
     tiles[2] = (int32_t)tile_capacity;
-    tiles[3] = 0;
+    tiles[3] = group ? n_pure : n_tiles;
   }
   __syncthreads();
 }
@@ -400,8 +457,9 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   }
   if constexpr (kFusedV > 0) {
     __shared__ int s_tot[2 * 4 * kScatterThreads];
-    __shared__ int s_wave[2 * kScatterThreads / 64];
-    fused_bases<kFusedV>(chunk_hist, (int64_t)gridDim.x, n_experts, chunk, block_m, tile_capacity, expert_offsets,
+    __shared__ int s_wave[3 * kScatterThreads / 64];
+    fused_bases<kFusedV>(chunk_hist, (int64_t)gridDim.x, n_experts, chunk, block_m, tile_capacity,
+                         dim >= kGroupTilesMinDim, expert_offsets,
                          tiles, cnt, s_tot, s_wave);
   } else {
     // the chunk's first slot per expert: its range's base plus the earlier
@@ -509,7 +567,7 @@ __global__ __launch_bounds__(256) void dense_tiles_kernel(
     tiles[0] = (int32_t)n_tiles;
     tiles[1] = block_m;
     tiles[2] = (int32_t)tile_capacity;
-    tiles[3] = 0;
+    tiles[3] = (int32_t)(n_tiles - n_tiles % kTileGroup);  // one expert: whole groups first already
     if (offsets != nullptr) {
       offsets[0] = 0;
       offsets[1] = (int32_t)n_rows;
@@ -586,9 +644,10 @@ int launch_permute(const int32_t* topk_idx, const void* topk_w,
                          dim3(256), 0, s, range_base, n_ranges, n_experts);
       if ((rc = check_launch("block_prefix_kernel"))) return rc;
     }
-    hipLaunchKernelGGL(scan_kernel, dim3(1), dim3(kScanThreads), 0, s,
+    hipLaunchKernelGGL(block_ranges > 0 ? scan_kernel<true> : scan_kernel<false>, dim3(1), dim3(kScanThreads), 0, s,
                        range_chunks > 1 || block_ranges > 0 ? range_base : chunk_hist, scan_rows, row_step,
-                       n_ranges, n_experts, block_m, tile_capacity, expert_offsets, range_base, tiles);
+                       n_ranges, n_experts, block_m, tile_capacity, dim >= kGroupTilesMinDim, expert_offsets,
+                       range_base, tiles);
     rc = check_launch("scan_kernel");
     if (rc || nc == 0) return rc;
   }

@@ -30,7 +30,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 KERNEL_NAMES = ["moe_route", "moe_permute", "moe_gemm_gate_up", "moe_gemm_down", "moe_combine"]
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 LIB_PATH = Path(os.environ.get("ASTRAI_MOE_LIB", Path(__file__).resolve().parent / "libastrai_moe.so"))
 
 _c_i32p = ctypes.POINTER(ctypes.c_int32)

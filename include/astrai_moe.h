@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define ASTRAI_MOE_ABI_VERSION 9
+#define ASTRAI_MOE_ABI_VERSION 10
 
 /* Element types. */
 #define ASTRAI_MOE_F32 0
@@ -56,11 +56,20 @@ extern "C" {
  * grouped GEMMs (int32):
  *   tiles[0] = number of row tiles (device-written)
  *   tiles[1] = block_m (rows per tile)
- *   tiles[2] = capacity (max tiles the array holds), tiles[3] = 0
+ *   tiles[2] = capacity (max tiles the array holds)
+ *   tiles[3] = first tile of the list's tail (see below)
  *   then per tile i: tiles[4+3i] = expert, tiles[5+3i] = first permuted row,
  *                    tiles[6+3i] = end of that expert's rows (exclusive).
  * Tiles never straddle experts, so an expert with M rows has ceil(M/block_m)
- * tiles and an expert with no rows has none. */
+ * tiles and an expert with no rows has none. Order: for dim >= 3072, each
+ * expert's first 8 * floor(n/8) tiles (n = its tile count) in expert order,
+ * then, as the tail, every expert's remaining tiles in expert order (the
+ * GEMMs walk row tiles in groups of 8, so that a group holds one expert's
+ * tiles); tiles[3] = the number of grouped tiles. For narrower rows the
+ * tiles are in expert order and tiles[3] = the tile count (no tail). The
+ * 256-row GEMM kernels let padding-only waves of tiles with 48 or more K
+ * steps idle only in the tail. Any order and any tiles[3] are valid inputs
+ * to the GEMMs: results do not depend on them. */
 #define ASTRAI_MOE_TILE_HEADER 4
 #define ASTRAI_MOE_TILE_STRIDE 3
 

@@ -99,6 +99,8 @@ PERM_CASES = [
     (100003, 32, 4, 72, 32),  # ragged last chunk; rows copied element-wise (72 x 2 bytes is not 16-byte aligned)
     (262144, 1024, 8, 16, 256),  # two-level scan over 4 groups of 256 expert columns
     (8448, 1024, 2, 16, 64),  # 33 ranges: a last block holding a single range
+    (1000, 3, 2, 4096, 64),  # rows of 4096: grouped tile order, scan folded into the scatter
+    (40000, 64, 6, 3072, 256),  # rows of 3072: grouped tile order written by the scan kernel (ranges)
 ]
 
 
@@ -118,14 +120,21 @@ def test_permute_bit_exact(gpu, n_tok, n_exp, top_k, dim, block_m):
     pos = torch.empty_like(perm.token_pos)
     pos[toks, slots] = torch.arange(toks.numel(), device=gpu, dtype=torch.int32)
     assert torch.equal(perm.token_pos, pos)
-    # Tile list: ceil(count / block_m) tiles per expert, in expert order.
+    # Tile list: ceil(count / block_m) tiles per expert. Rows of 3072 or more
+    # elements: every expert's whole groups of 8 tiles first (expert order),
+    # then the tiles left over (expert order), tiles[3] = the number of
+    # grouped tiles; narrower rows: expert order, tiles[3] = the tile count.
     tl = perm.tiles.cpu().tolist()
     counts = (offs[1:] - offs[:-1]).tolist()
-    expect = []
+    grouped, left = [], []
     for e, c in enumerate(counts):
-        for j in range(-(-c // block_m)):
-            expect.append([e, offs[e].item() + j * block_m, offs[e + 1].item()])
+        n = -(-c // block_m)
+        n_grouped = n - n % 8 if dim >= 3072 else 0
+        for j in range(n):
+            (grouped if j < n_grouped else left).append([e, offs[e].item() + j * block_m, offs[e + 1].item()])
+    expect = grouped + left
     assert tl[0] == len(expect) and tl[1] == block_m
+    assert tl[3] == (len(grouped) if dim >= 3072 else len(expect))
     got = [tl[4 + 3 * i: 7 + 3 * i] for i in range(tl[0])]
     assert got == expect
 
@@ -581,7 +590,7 @@ def test_dense_expert_tile_list_and_gemms(gpu, n_tok, dim, dim_ffn, dtype):
     bm = ops.dense_block_m(n_tok, dim, dim_ffn, dtype)
     tiles, offsets = ops.dense_tiles(n_tok, bm, gpu, with_offsets=True)
     n = -(-n_tok // bm)
-    want = [n, bm, n, 0] + [v for i in range(n) for v in (0, i * bm, n_tok)]
+    want = [n, bm, n, n - n % 8] + [v for i in range(n) for v in (0, i * bm, n_tok)]
     torch.cuda.synchronize()
     assert tiles.tolist() == want and offsets.tolist() == [0, n_tok]
     g = torch.Generator(device=gpu).manual_seed(5)

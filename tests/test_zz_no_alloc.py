@@ -56,14 +56,15 @@ def test_noalloc_permute_matches_workspace_permute(gpu):
     # (tokens, experts, top_k, dim, dtype, block_m, copy rows). Histograms of
     # more than 32768 counts (chunks of 32 tokens x experts) take the scan
     # that keeps per-range expert bases in the library's scratch (ranges of 8
-    # chunks): the first case writes 157 range rows x 64 experts, the second
+    # chunks): the first case writes 157 range rows x 64 experts (rows of
+    # 3072: the grouped tile order), the second
     # a smaller problem over the same experts (79 rows: it must not see the
     # first call's bases past them), the third another expert count (36 rows
     # x 128), the fourth 33 rows x 1024 scanned in two levels (blocks of 32
     # ranges). The last two are small enough for the scan folded into the
     # scatter, which needs no scratch.
     cases = [
-        (40000, 64, 6, 256, torch.bfloat16, 256, False),
+        (40000, 64, 6, 3072, torch.bfloat16, 256, False),
         (20000, 64, 6, 128, torch.bfloat16, 256, True),
         (9000, 128, 8, 256, torch.bfloat16, 128, False),
         (8448, 1024, 2, 64, torch.bfloat16, 64, True),
