@@ -375,12 +375,14 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
 // about an atomic's round trip, so claims are made only where tiles are long
 // (kDynamicMinSteps): measured against the static deal, in one process with
 // the builds alternating, the Mixtral-shaped GEMMs (64 and 224 steps per
-// tile) gained 1.8 % (gate/up) and 0.8 % (down), while the fine-grained
-// shape (32 and 22 steps) lost 0.4 % and 2.4 %.
+// tile) gained 1.8 % (gate/up) and 0.8 % (down). At the fine-grained shape
+// the 32-step gate/up tiles gained 2.3-2.7 % (1.1-1.2 % with the skewed
+// router) once padding-only waves idled, and the 22-step down tiles lost
+// 1.3-1.7 %.
 constexpr int kMailboxBase = 64;       // int32 offset of the mailboxes in the scheduling block
 constexpr int kMaxSchedGroups = 1024;  // workgroups the scheduling block has mailboxes for
 constexpr int kDynamicShare = 10;      // 1 / kDynamicShare of the items are claimed at run time
-constexpr int kDynamicMinSteps = 48;   // K steps per tile from which items are claimed at run time
+constexpr int kDynamicMinSteps = 32;   // K steps per tile from which items are claimed at run time
 constexpr int kClaimLead = 6;
 static_assert(kClaimLead > 4 && kClaimLead < kSplitMinSteps, "claim between the DMA waves' lead and an item's end");
 

@@ -255,14 +255,15 @@ def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
 @pytest.mark.parametrize("n_tok,n_exp,top_k,dim,dim_ffn,packed", [
     (8192, 8, 2, 1024, 4096, False),  # ~68 row tiles x 4 column tiles: a short last round, split 8 ways
     (8192, 8, 2, 1024, 4096, True),
-    (6144, 8, 2, 2048, 1408, False),  # ~52 x 8: 22 K steps per tile, too short to split
+    (6144, 8, 2, 2048, 1408, False),  # ~52 x 8: 22 K steps per down tile, too short to split; gate/up
+                                      # 32 steps: claims
     (16384, 1, 1, 512, 4096, False),  # one expert: 64 row tiles x 2 = 128 tiles, a partial first round
     (4096, 4, 2, 256, 1024, False),  # 32 row tiles x 1 column tile
-    # 48 K steps or more per tile: the last tenth of the items claimed at run time
+    # 32 K steps or more per tile: the last tenth of the items claimed at run time
     (16384, 8, 2, 3072, 1024, False),  # gate/up: ~132 row tiles x 8 column tiles
     (16384, 8, 2, 3072, 1024, True),
     (24576, 8, 2, 1024, 4096, False),  # down: ~196 x 4, with a split tail
-    (24576, 16, 2, 512, 2048, False),  # ~200 x 2 down / x 16 gate/up, 32 steps: every tile dealt in advance
+    (24576, 16, 2, 512, 2048, False),  # ~200 x 2 down (32 steps: claims) / x 16 gate/up (8 steps: static)
 ])
 def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
     """The 256-row GEMMs with their workspace (the last tenth of the tiles
