@@ -14,9 +14,16 @@ unchanged. Models built before the call keep the classes they were built with.
     from astrai_amd.integration import use_hip_ffn
     use_hip_ffn()                 # before the model is built
     model = AutoModel.from_pretrained(path)   # astrai/model/automodel.py:54
+
+``register_kernels`` makes AstrAI's own kernel discovery
+(``astrai/extension/loader.py:14-36``) list this package's kernels, so that
+``astrai.extension.loader.is_available("moe_route")`` and ``get_module`` answer
+for them and ``import astrai.extension.moe_route`` finds them.
 """
 
 from __future__ import annotations
+
+import sys
 
 from astrai_amd.model.components.mlp import MLP, DeepSeekMoE
 
@@ -57,3 +64,36 @@ def restore_ffn(previous: dict, factory=None) -> None:
             entries.pop(name, None)
         else:
             entries[name] = cls
+
+
+def register_kernels(ext_loader=None) -> list[str]:
+    """Add this package's available kernels (``astrai_amd.extension.loader``)
+    to a kernel loader with the reference's interface (default: AstrAI's
+    ``astrai.extension.loader``): each name is appended to its
+    ``KERNEL_NAMES``, marked in ``_available`` and given its module handle in
+    ``_modules`` (the dicts its ``is_available`` / ``get_module`` read; the
+    reference fills them once, at import, from ``KERNEL_NAMES``), and the
+    handle is importable as ``<loader package>.<name>``, the submodule the
+    reference's discovery imports. Unavailable kernels are left out. Returns
+    the names registered."""
+    from astrai_amd.extension import loader as ours
+
+    if ext_loader is None:
+        from astrai.extension import loader as ext_loader  # the reference's discovery
+    for attr in ("KERNEL_NAMES", "_available", "_modules"):
+        if not hasattr(ext_loader, attr):
+            raise TypeError(f"{ext_loader!r} has no {attr}: not a kernel loader with the reference's interface")
+    package = ext_loader.__package__ or ext_loader.__name__.rpartition(".")[0]
+    names = []
+    for name in ours.KERNEL_NAMES:
+        if not ours.is_available(name):
+            continue
+        handle = ours.get_module(name)
+        if name not in ext_loader.KERNEL_NAMES:
+            ext_loader.KERNEL_NAMES.append(name)
+        ext_loader._available[name] = True
+        ext_loader._modules[name] = handle
+        if package:
+            sys.modules[f"{package}.{name}"] = handle
+        names.append(name)
+    return names

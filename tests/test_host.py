@@ -464,6 +464,45 @@ def test_use_hip_ffn_swaps_the_registry_entries():
     assert "moe" not in Other._entries
 
 
+def test_register_kernels_reaches_a_reference_style_loader():
+    # a stand-in with the reference's discovery interface
+    # (astrai/extension/loader.py:14-36): KERNEL_NAMES, _available and
+    # _modules filled at import, is_available / get_module reading them, and
+    # kernels imported as <package>.<name> submodules
+    import importlib
+    import sys
+    import types
+
+    from astrai_amd.integration import register_kernels
+
+    pkg = types.ModuleType("fake_astrai_ext")
+    pkg.__path__ = []
+    ext = types.ModuleType("fake_astrai_ext.loader")
+    ext.__package__ = "fake_astrai_ext"
+    ext.KERNEL_NAMES = ["attn_decode"]
+    ext._available = {"attn_decode": False}
+    ext._modules = {"attn_decode": None}
+    ext.is_available = lambda name: ext._available.get(name, False)
+    ext.get_module = lambda name: ext._modules.get(name)
+    sys.modules["fake_astrai_ext"], sys.modules["fake_astrai_ext.loader"] = pkg, ext
+    try:
+        names = register_kernels(ext)
+        assert names == [n for n in loader.KERNEL_NAMES if loader.is_available(n)]
+        assert loader.is_available("moe_route"), loader.load_error()  # the library loads without a GPU
+        for name in names:
+            assert ext.is_available(name) and name in ext.KERNEL_NAMES
+            assert ext.get_module(name) is loader.get_module(name)
+            assert callable(getattr(ext.get_module(name), name))
+            assert importlib.import_module(f".{name}", package="fake_astrai_ext") is loader.get_module(name)
+        assert ext.KERNEL_NAMES[0] == "attn_decode" and not ext.is_available("attn_decode")
+        assert register_kernels(ext) == names and ext.KERNEL_NAMES.count("moe_route") == 1  # idempotent
+        with pytest.raises(TypeError):
+            register_kernels(types.ModuleType("not_a_loader"))
+    finally:
+        for key in [k for k in sys.modules if k == "fake_astrai_ext" or k.startswith("fake_astrai_ext.")]:
+            del sys.modules[key]
+
+
 # -- register allocation of the matrix-core GEMMs (device code compiled here) ----
 
 
