@@ -100,11 +100,22 @@ __device__ __forceinline__ int64_t block_row(int64_t b, int64_t row_step, int64_
 __device__ __forceinline__ int grouped_tiles(int ntile, bool group) {
   return group ? ntile - ntile % kTileGroup : 0;
 }
-// Position of tile j of an expert: the grouped head (pure0: the expert's
-// first tile there, the exclusive prefix of grouped tiles) or the tail
-// (left0: its first tile there), each in expert order.
-__device__ __forceinline__ int64_t tile_slot(int j, int npure, int64_t pure0, int64_t left0) {
-  return j < npure ? pure0 + j : left0 + (j - npure);
+// Tiles j0 .. j1 - 1 of expert e (rows [row0, row_end)) at list positions
+// slot0, slot0 + 1, ... (those below the capacity). An expert's tiles
+// [0, npure) go to the grouped head at pure0 (the exclusive prefix of grouped
+// tiles), the rest to the tail at n_pure + the earlier experts' leftover
+// tiles, each part in expert order. (Two plain loops: a select per tile
+// between the two places made the permutation ~2 us slower at 8 experts.)
+__device__ __forceinline__ void write_expert_tiles(int32_t* tiles, int64_t capacity, int e, int row0, int row_end,
+                                                   int block_m, int j0, int j1, int64_t slot0) {
+  const int n = (int)min((int64_t)(j1 - j0), max(capacity - slot0, (int64_t)0));
+  int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER + slot0 * ASTRAI_MOE_TILE_STRIDE;
+#pragma unroll 1
+  for (int i = 0; i < n; ++i, t += ASTRAI_MOE_TILE_STRIDE) {
+    t[0] = e;
+    t[1] = row0 + (j0 + i) * block_m;
+    t[2] = row_end;
+  }
 }
 
 // Grid (blocks of kBlockRanges ranges, groups of 256 experts): each range's
@@ -246,14 +257,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       tiles[3] = group ? n_pure : tile_incl;
     }
     // the expert's row tiles (stores only: nothing waits on them)
-    for (int j = 0; j < ntile; ++j) {
-      const int64_t slot = tile_slot(j, npure, pure0, left0);
-      if (slot >= tile_capacity) continue;
-      int32_t* t = tiles + ASTRAI_MOE_TILE_HEADER + slot * ASTRAI_MOE_TILE_STRIDE;
-      t[0] = threadIdx.x;
-      t[1] = off + j * block_m;
-      t[2] = off + cnt;
-    }
+    write_expert_tiles(tiles, tile_capacity, threadIdx.x, off, off + cnt, block_m, 0, npure, pure0);
+    write_expert_tiles(tiles, tile_capacity, threadIdx.x, off, off + cnt, block_m, npure, ntile, left0);
   }
   __syncthreads();
 
@@ -374,18 +379,25 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
     run += tot4[j];
   }
   const bool write_list = blockIdx.x == 0 && blockIdx.y == 0;
-  int ntile_run = 0, pure_run = 0;
+  int ntile_run = 0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int nt = (tot4[j] + block_m - 1) / block_m;
-    ntile_run += nt;
-    pure_run += grouped_tiles(nt, group);
+  for (int j = 0; j < 4; ++j) ntile_run += (tot4[j] + block_m - 1) / block_m;
+  // exclusive prefixes over experts of rows and tiles
+  int pre[2] = {run, ntile_run}, tot[2];
+  scatter_block_exclusive_scan<2>(pre, s_wave, tot);
+  int off = pre[0], tile0 = pre[1];
+  const int n_rows = tot[0], n_tiles = tot[1];
+  // and of the tiles in whole groups, for the workgroup that writes the list
+  // (uniform over the workgroup: its barriers are safe)
+  int pure0 = 0, n_pure = 0;
+  if (write_list && group) {
+    int pure[1] = {0}, pure_tot[1];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pure[0] += grouped_tiles((tot4[j] + block_m - 1) / block_m, true);
+    __syncthreads();  // the previous scan's reads of s_wave are done
+    scatter_block_exclusive_scan<1>(pure, s_wave, pure_tot);
+    pure0 = pure[0], n_pure = pure_tot[0];
   }
-  // exclusive prefixes over experts of rows, tiles and whole-group tiles
-  int pre[3] = {run, ntile_run, pure_run}, tot[3];
-  scatter_block_exclusive_scan<3>(pre, s_wave, tot);
-  int off = pre[0], tile0 = pre[1], pure0 = pre[2];
-  const int n_rows = tot[0], n_tiles = tot[1], n_pure = tot[2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = 4 * t + j;
@@ -395,15 +407,9 @@ __device__ void fused_bases(const int32_t* __restrict__ chunk_hist, int64_t nc, 
         expert_offsets[e] = off;
         const int ntile = (tot4[j] + block_m - 1) / block_m;
         const int npure = grouped_tiles(ntile, group);
-        const int64_t left0 = (int64_t)n_pure + (tile0 - pure0);
-        for (int k = 0; k < ntile; ++k) {
-          const int64_t slot = tile_slot(k, npure, pure0, left0);
-          if (slot >= tile_capacity) continue;
-          int32_t* tt = tiles + ASTRAI_MOE_TILE_HEADER + slot * ASTRAI_MOE_TILE_STRIDE;
-          tt[0] = e;
-          tt[1] = off + k * block_m;
-          tt[2] = off + tot4[j];
-        }
+        write_expert_tiles(tiles, tile_capacity, e, off, off + tot4[j], block_m, 0, npure, pure0);
+        write_expert_tiles(tiles, tile_capacity, e, off, off + tot4[j], block_m, npure, ntile,
+                           n_pure + (tile0 - pure0));
         tile0 += ntile;
         pure0 += npure;
       }
@@ -457,7 +463,7 @@ __global__ __launch_bounds__(kScatterThreads) void scatter_kernel(
   }
   if constexpr (kFusedV > 0) {
     __shared__ int s_tot[2 * 4 * kScatterThreads];
-    __shared__ int s_wave[3 * kScatterThreads / 64];
+    __shared__ int s_wave[2 * kScatterThreads / 64];
     fused_bases<kFusedV>(chunk_hist, (int64_t)gridDim.x, n_experts, chunk, block_m, tile_capacity,
                          dim >= kGroupTilesMinDim, expert_offsets,
                          tiles, cnt, s_tot, s_wave);
