@@ -94,7 +94,9 @@ def test_graph_shapes(gpu, dim, dim_ffn, n_exp, n_shared, top_k, dtype, n_tok):
 
 
 @pytest.mark.parametrize("dim,dim_ffn,n_tok", [
-    (3072, 1024, 8192),  # gate/up: 48 K steps, the last tenth of ~544 tiles claimed at run time
+    (3072, 1024, 8192),  # gate/up: 48 K steps, the last tenth of ~544 tiles claimed at run time;
+                         # the tile list in whole groups of one expert
+    (2048, 1536, 8192),  # gate/up: 32 K steps, claims with padding-only waves idle in every tile
     (1024, 4096, 8192),  # down: 64 K steps, claims and a split last round (fp32 partials, ordered reduce)
 ])
 def test_graph_run_time_claims_and_split_tail(gpu, dim, dim_ffn, n_tok):

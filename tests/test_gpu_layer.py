@@ -166,8 +166,13 @@ def test_partial_column_tiles(gpu, dim, dim_ffn, n_exp, n_shared, top_k, n_tok):
 
 @pytest.mark.parametrize("name,n_tokens", [
     ("moe_bf16_d2048_f1408_e64_k6_t8192", 1024),
+    # 32-step gate/up tiles: the last tenth handed out at run time, padding-only
+    # waves idle in every tile
+    ("moe_bf16_d2048_f1408_e64_k6_t8192_zipf", None),
     # 64 and 224 K steps per tile: the gate/up GEMM hands out its last tenth
-    # at run time and the down GEMM splits its partial last round along K
+    # at run time and the down GEMM splits its partial last round along K;
+    # the tile list in whole groups of one expert, padding-only waves idle in
+    # its tail
     ("moe_bf16_d4096_f14336_e8_k2_t16384", None),
 ])
 def test_deterministic_repeat(gpu, name, n_tokens):
