@@ -264,8 +264,12 @@ def _tail_split(n_live, n_tiles_n, capacity, ksteps, cus):
     (16384, 8, 2, 3072, 1024, True),
     (24576, 8, 2, 1024, 4096, False),  # down: ~196 x 4, with a split tail
     (24576, 16, 2, 512, 2048, False),  # ~200 x 2 down (32 steps: claims) / x 16 gate/up (8 steps: static)
+    # skewed routers (a Zipf-like bias: hot experts, empty ones) on rows of 3072+ elements: the tile list
+    # in whole groups of one expert with a tail of leftover tiles, padding-only waves idle in the tail
+    pytest.param(16384, 16, 2, 3072, 1024, False, id="skewed-grouped-gate_up48"),
+    pytest.param(16384, 8, 2, 3072, 4096, False, id="skewed-grouped-both64-split"),
 ])
-def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed):
+def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_ffn, packed, request):
     """The 256-row GEMMs with their workspace (the last tenth of the tiles
     claimed at run time; the down GEMM's last round split along K, partial
     sums reduced in slice order) against the same GEMMs with every tile dealt
@@ -274,7 +278,12 @@ def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_
     bit-identical and the tail within the GEMM tolerance, and the train
     variants' outputs bit-identical to the inference ones."""
     dtype = torch.bfloat16
-    route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=11)
+    if "skewed" in request.node.callspec.id:
+        logits = _logits(gpu, n_tok, n_exp, torch.float32, 1.0, 11)
+        rank = torch.randperm(n_exp, generator=torch.Generator().manual_seed(3)).to(gpu) + 1
+        route = ops.moe_route((logits - 3.0 * torch.log(rank.float())).to(dtype), top_k)
+    else:
+        route = _routing(gpu, n_tok, n_exp, top_k, dtype, seed=11)
     g = torch.Generator(device=gpu).manual_seed(4)
     x = torch.randn(n_tok, dim, generator=g, device=gpu).to(dtype)
     experts = _experts(gpu, n_exp, dim, dim_ffn, dtype, seed=6)
@@ -307,7 +316,15 @@ def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_
     cus = torch.cuda.get_device_properties(gpu).multi_processor_count
     n_tiles_n = -(-dim // 256)
     left, s = _tail_split(n_live, n_tiles_n, capacity, dim_ffn // 64, cus)
-    print(f"{n_live} row tiles x {n_tiles_n}: {left} tail tiles split {s} ways", flush=True)
+    counts = (perm.expert_offsets[1:] - perm.expert_offsets[:-1]).tolist()
+    print(f"{n_live} row tiles x {n_tiles_n}: {left} tail tiles split {s} ways; rows per expert {counts}; "
+          f"grouped tiles {tl[3]}", flush=True)
+    if "skewed" in request.node.callspec.id:
+        # the case it is for: (nearly) empty experts, hot ones with whole groups, a tail with tiles of at
+        # most 128 rows
+        assert min(counts) <= 16 and tl[3] >= 16 and tl[3] < n_live
+        tail_rows = [min(256, tl[6 + 3 * i] - tl[5 + 3 * i]) for i in range(tl[3], n_live)]
+        assert min(tail_rows) <= 128, tail_rows
     # which (row tile, column tile) blocks differ between the split and whole orders
     row_tile = torch.full((h.shape[0],), -1, dtype=torch.long)
     for i in range(n_live):
@@ -327,6 +344,10 @@ def test_gemm_run_time_claims_and_split_tail(gpu, n_tok, n_exp, top_k, dim, dim_
             continue
         y_ref = F.linear(h[a:b], w.down) * perm.sorted_w[a:b].unsqueeze(-1)  # mlp.py:24, :97
         torch.testing.assert_close(y[a:b], y_ref, **BF16_TOL)
+        if "skewed" in request.node.callspec.id:
+            xe = perm.x_perm[a:b]
+            h_ref = (F.silu(F.linear(xe, w.gate)) * F.linear(xe, w.up))  # mlp.py:22-23
+            torch.testing.assert_close(h[a:b], h_ref, **BF16_TOL)
     if not packed:
         h_tr, _ = ops.moe_gemm_gate_up_train(perm.x_perm, perm.tiles, tg, tu, n_exp, dim_ffn)
         y_tr, y_unw = ops.moe_gemm_down_train(h, perm.tiles, td, perm.sorted_w, n_exp, dim)
