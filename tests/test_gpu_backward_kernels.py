@@ -65,6 +65,9 @@ CASES = [
     (3000, 8, 2, 256, 640, 3.0, BF),  # skewed: one expert holds most rows
     (1024, 8, 2, 704, 576, 0.0, BF),  # dims multiples of 64 only: partial last column tiles everywhere
     (300, 8, 4, 192, 320, 1.0, BF),
+    # rows of 3072: the tile list in whole groups of one expert (the skew gives the hot expert several),
+    # dgrad_down's 48-step tiles let padding-only waves idle in the list's tail only
+    (6000, 8, 2, 3072, 512, 3.0, BF),
     # general-shape kernels
     (300, 8, 2, 40, 24, 0.0, BF),  # the reference's tiny-config scale
     (200, 4, 2, 37, 30, 0.0, BF),  # dim_ffn % 4 == 2: a 2-column last block of g/u
