@@ -72,6 +72,16 @@ def test_workload_layer(gpu, name):
         assert (counts == 0).sum().item() >= 3
 
 
+@pytest.mark.parametrize("n_tokens", [64, 700, 2048, 8192, 9000])
+def test_mixtral_shape_token_counts(gpu, n_tokens):
+    # the Mixtral-shaped weights at prefill and decode sizes: 32- to 256-row
+    # tiles; from ~1 000 rows per expert whole groups of 8 row tiles (the
+    # tile list's grouped head) and a tail of leftover tiles, padding-only
+    # waves idle there
+    layer, x = make_layer(WORKLOADS["moe_bf16_d4096_f14336_e8_k2_t16384"], gpu, n_tokens=n_tokens)
+    check_layer(layer, x, f"Mixtral shape, tokens={n_tokens}")
+
+
 @pytest.mark.parametrize("n_tokens", [1, 31, 33, 129])
 def test_small_token_counts(gpu, n_tokens):
     layer, x = make_layer(WORKLOADS["moe_bf16_d2048_f1408_e64_k6_t8192"], gpu, n_tokens=n_tokens)
