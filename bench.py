@@ -30,6 +30,9 @@ Prints one JSON line:
                   of the same inputs (every intermediate unrounded): each
                   one's plain-tolerance failures, max normalised and RMS
                   error (truth_*)
+  vs_hipblaslt    (--vs-hipblaslt) the grouped GEMMs' TFLOP/s against
+                  torch's F.linear (hipBLASLt) per expert on the same rows
+                  and weights, on the workload's routing and a balanced one
 """
 
 from __future__ import annotations
@@ -83,6 +86,10 @@ def _parse():
                    help="also time the step as a replayed HIP graph (reported as graph_*; value stays eager)")
     p.add_argument("--pack", action="store_true",
                    help="read the layer's packed inference copy of the expert weights (opt-in)")
+    p.add_argument("--vs-hipblaslt", action="store_true",
+                   help="also time the grouped GEMMs against torch's F.linear (hipBLASLt) per expert on the same "
+                        "rows and weights, on the workload's routing and on a balanced one (reported as "
+                        "vs_hipblaslt)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="before timing, copy a buffer of this many MiB once (a plain copy kernel of known size "
                         "that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -243,6 +250,70 @@ def cpu_baseline(layer, x, w, target_s: float) -> dict:
                   f"path (mlp.py:79-100) on CPU in {str(w.dtype).replace('torch.', '')}, {dt:.1f} s",
         **host,
     }
+
+
+def _median_ms(fn, n: int = 12) -> float:
+    ts = []
+    for _ in range(n):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        fn()
+        e.record()
+        e.synchronize()
+        ts.append(s.elapsed_time(e))
+    ts = ts[2:]
+    return sorted(ts)[len(ts) // 2]
+
+
+def vs_hipblaslt(layer, x, w, ops) -> dict | None:
+    """The layer's grouped gate/up (gathering x) and down GEMMs against
+    torch's F.linear, i.e. hipBLASLt, run once per expert on the same
+    permuted rows and weights (gate and up concatenated into one [2F, D]
+    weight, so hipBLASLt's gate/up is one GEMM per expert without the SwiGLU,
+    which the grouped kernel fuses): on the workload's routing, and on a
+    routing that gives every expert exactly T*k/E rows (token t's j-th slot
+    to expert (t*k + j) mod E; whole 256-row tiles when 256 divides it).
+    bf16 workloads on 256-row tiles only. Medians of 10 timed calls."""
+    import torch.nn.functional as F
+
+    T, E, K, D, Fd = w.n_tokens, w.n_experts, w.top_k, w.dim, w.dim_ffn
+    if w.dtype != torch.bfloat16 or ops.select_block_m(T, E, K, D, Fd, w.dtype) != 256:
+        return None
+    x2 = x.view(-1, D)
+    experts = layer.routed_experts
+    tg = ops.expert_weight_table([m.gate.weight for m in experts], (Fd, D))
+    tu = ops.expert_weight_table([m.up.weight for m in experts], (Fd, D))
+    td = ops.expert_weight_table([m.down.weight for m in experts], (D, Fd))
+    w_gu = [torch.cat([m.gate.weight, m.up.weight]) for m in experts]
+    w_dn = [m.down.weight for m in experts]
+    fl_gu, fl_dn = 4.0 * T * K * D * Fd, 2.0 * T * K * D * Fd
+
+    def leg(route) -> dict:
+        perm = ops.moe_permute(route, x2, E, 256)
+        offs = perm.expert_offsets.tolist()
+        h = ops.moe_gemm_gate_up_gather(x2, perm.sorted_token, perm.tiles, tg, tu, E, Fd, 256)
+        ours_gu = _median_ms(lambda: ops.moe_gemm_gate_up_gather(x2, perm.sorted_token, perm.tiles, tg, tu, E, Fd, 256))
+        ours_dn = _median_ms(lambda: ops.moe_gemm_down(h, perm.tiles, td, perm.sorted_w, E, D, 256))
+        spans = [(e, offs[e], offs[e + 1]) for e in range(E) if offs[e + 1] > offs[e]]
+        blas_gu = _median_ms(lambda: [F.linear(perm.x_perm[a:b], w_gu[e]) for e, a, b in spans])
+        blas_dn = _median_ms(lambda: [F.linear(h[a:b], w_dn[e]) for e, a, b in spans])
+        return {
+            "rows_per_expert": [b - a for _, a, b in spans],
+            "grouped_gate_up_tflops": fl_gu / ours_gu / 1e9, "grouped_down_tflops": fl_dn / ours_dn / 1e9,
+            "hipblaslt_gate_up_tflops": fl_gu / blas_gu / 1e9, "hipblaslt_down_tflops": fl_dn / blas_dn / 1e9,
+            "grouped_over_hipblaslt_both": (blas_gu + blas_dn) / (ours_gu + ours_dn),
+        }
+
+    with torch.inference_mode():
+        real = leg(ops.moe_route(layer.router(x2), K))
+        slots = (torch.arange(T, device=x.device).unsqueeze(1) * K + torch.arange(K, device=x.device)) % E
+        logits = torch.full((T, E), -8.0, device=x.device)
+        logits.scatter_(1, slots, torch.linspace(2.0, 1.0, K, device=x.device).expand(T, K).contiguous())
+        balanced = leg(ops.moe_route(logits.to(w.dtype), K))
+    torch.cuda.synchronize()
+    return {"workload_routing": real, "balanced_routing": balanced,
+            "timing": "HIP events around each call (hipBLASLt: one F.linear per expert), median of 10",
+            "note": "hipBLASLt's gate/up omits the SwiGLU and its down the routing weight; the grouped kernels fuse both"}
 
 
 def main():
@@ -459,6 +530,8 @@ def main():
     if graph_ms is not None:
         result["graph_ms_per_step"] = graph_ms
         result["graph_value"] = T / (graph_ms / 1e3)
+    if args.vs_hipblaslt:
+        result["vs_hipblaslt"] = vs_hipblaslt(layer, x, w, ops)
     if not args.no_parity:
         result["parity"] = parity_leg(layer, x, w, ops)
     if not args.no_cpu_baseline:
