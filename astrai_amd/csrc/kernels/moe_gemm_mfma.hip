@@ -582,6 +582,19 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
     uint32_t nA = 0, nB = 0;
     static_for<16 / RG>([&](auto gg) {
       constexpr int r0 = decltype(gg)::value * RG;
+      // Issue priority falls as a wave gets through the step, so that of the
+      // two matrix-core waves on a SIMD the one behind takes the matrix core.
+      // At equal priority the older wave issued first: it reached the step
+      // barrier well ahead (~35 % of the step in per-step cycle counts), and
+      // the other then issued its last rows alone, where its own fragment
+      // reads left gaps. Measured in one process, builds alternating,
+      // bit-identical: gate/up +2.1 to +2.5 % (Mixtral shape), +2.7 to
+      // +3.2 % (fine-grained shape), down +2.4 to +3.4 % with the drop at
+      // row 10; the drop at row 8 left the down GEMM as it was, the drop at
+      // row 10 made the gathering gate/up GEMM's tile changes spill.
+      constexpr int kPrioDrop = kGateUp ? 8 : 10;
+      if constexpr (r0 == 0) __builtin_amdgcn_s_setprio(1);
+      if constexpr (r0 == kPrioDrop) __builtin_amdgcn_s_setprio(0);
       if constexpr (r0 + PD >= 16 && r0 + PD < 16 + RG) {
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();  // X_g
