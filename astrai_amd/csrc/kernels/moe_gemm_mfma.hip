@@ -587,14 +587,18 @@ __global__ __launch_bounds__(StreamCfg<kGateUp>::THREADS, 1) void gemm_stream_ke
       // At equal priority the older wave issued first: it reached the step
       // barrier well ahead (~35 % of the step in per-step cycle counts), and
       // the other then issued its last rows alone, where its own fragment
-      // reads left gaps. Measured in one process, builds alternating,
-      // bit-identical: gate/up +2.1 to +2.5 % (Mixtral shape), +2.7 to
-      // +3.2 % (fine-grained shape), down +2.4 to +3.4 % with the drop at
-      // row 10; the drop at row 8 left the down GEMM as it was, the drop at
-      // row 10 made the gathering gate/up GEMM's tile changes spill.
-      constexpr int kPrioDrop = kGateUp ? 8 : 10;
+      // reads left gaps. gate/up: 1 from row 0, 0 from row 8, 1 for rows 10
+      // and 11, 0 from row 12; down: 1 from row 0, 0 from row 10, 1 from row
+      // 12. Measured in one process, builds alternating, bit-identical, with
+      // the single drop (row 8 gate/up, row 10 down): gate/up +2.1 to +2.5 %
+      // (Mixtral shape), +2.7 to +3.2 % (fine-grained shape), down +2.4 to
+      // +3.4 %; the later steps up and down added +0.3 to +0.7 % (Mixtral
+      // shape). Drops at rows 4, 6 or 12 alone made the gathering gate/up
+      // GEMM's tile changes spill; three levels (2, 1, 0) measured -0.5 to
+      // -3.8 %.
       if constexpr (r0 == 0) __builtin_amdgcn_s_setprio(1);
-      if constexpr (r0 == kPrioDrop) __builtin_amdgcn_s_setprio(0);
+      if constexpr (kGateUp ? (r0 == 8 || r0 == 12) : r0 == 10) __builtin_amdgcn_s_setprio(0);
+      if constexpr (kGateUp ? r0 == 10 : r0 == 12) __builtin_amdgcn_s_setprio(1);
       if constexpr (r0 + PD >= 16 && r0 + PD < 16 + RG) {
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();  // X_g
