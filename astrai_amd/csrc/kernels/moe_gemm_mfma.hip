@@ -75,6 +75,8 @@
 // tile (i, j) is output row 16 i + l % 16, column 16 j + 4 (l / 16) + r.
 #include "mfma_tile.h"
 
+#include <type_traits>
+
 
 namespace astrai_moe {
 namespace {
@@ -302,13 +304,23 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
   const int row_l = el & 15;
   const int q = el >> 4;
   const int n_base = kGateUp ? t_nt * (BN / 2) + wn * (WN / 2) : t_nt * BN + wn * WN;
+  // gate/up: the tile's first row as a uniform base and the lanes at 32-bit
+  // element offsets from it (a tile's rows hold at most 256 N elements, 512 N
+  // for S0, below 2^31 with the launchers' N <= 2^22): the saving kernel then
+  // keeps its addresses in registers (with 64-bit row offsets it spilled them
+  // and reloaded them between the stores; training gate/up +0.7 % at the
+  // Mixtral shape, bit-identical). The down kernels keep 64-bit offsets, which
+  // spilled less there.
+  using Off = std::conditional_t<kGateUp, uint32_t, int64_t>;
+  bf16_t* const Ct = kGateUp ? C + (int64_t)t_row0 * N : C;
+  bf16_t* const St = kSave && kGateUp ? S0 + (int64_t)t_row0 * N * 2 : S0;
 #pragma unroll
   for (int i = 0; i < MT16; ++i) {
     const int gm = wm * WM + i * 16 + row_l;
     const int srow = t_row0 + min(gm, t_rows - 1);
     float w = 1.0f;
     if (!kGateUp && row_w != nullptr) w = bf16_bits_to_f32(row_w[srow]);  // no row weights: 1
-    const int64_t row_off = (int64_t)srow * N + n_base;
+    const Off row_off = kGateUp ? (Off)(uint32_t)(min(gm, t_rows - 1) * N + n_base) : (Off)((int64_t)srow * N + n_base);
 #pragma unroll
     for (int jp = 0; jp < NJ; jp += 2) {
       // gate/up: h = bf16(u * bf16(silu(g))) per element, then transposed;
@@ -337,7 +349,7 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
             bf16x8_t gu;
 #pragma unroll
             for (int r = 0; r < 4; ++r) gu[r] = (__bf16)acc[i][j][r], gu[4 + r] = (__bf16)acc[i][j + NJ][r];
-            *reinterpret_cast<bf16x8_t*>(S0 + 2 * (row_off + j * 16 + 4 * q)) = gu;
+            *reinterpret_cast<bf16x8_t*>(St + (Off)2 * (row_off + j * 16 + 4 * q)) = gu;
           }
         }
       }
@@ -348,11 +360,11 @@ __device__ __forceinline__ void store_tile_direct(f32x4_t (&acc)[WM / 16][WN / 1
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] = o[0][r], v[4 + r] = o[1][r];
         if constexpr (!kGateUp) {
-          if constexpr (kSave) *reinterpret_cast<bf16x8_t*>(S0 + row_off + jp * 16 + 8 * q) = v;
+          if constexpr (kSave) *reinterpret_cast<bf16x8_t*>(St + (row_off + jp * 16 + 8 * q)) = v;
 #pragma unroll
           for (int c = 0; c < 8; ++c) v[c] = (__bf16)((float)v[c] * w);
         }
-        *reinterpret_cast<bf16x8_t*>(C + row_off + jp * 16 + 8 * q) = v;
+        *reinterpret_cast<bf16x8_t*>(Ct + (row_off + jp * 16 + 8 * q)) = v;
       }
     }
   }

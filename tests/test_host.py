@@ -530,20 +530,21 @@ def _device_kernel_metadata(src: Path, tmp_path: Path) -> dict:
 
 def test_matrix_core_gemms_keep_their_registers(tmp_path):
     """The 256-row kernels' K loops hold 128 accumulators, the operand rings
-    and the addresses in 168 VGPRs: the inference gate/up GEMMs (plain,
-    gathering, packed) and the dgrad_down / dgrad_in_add / wgrad kernels
-    must compile without spills (a change to the tile loop that made the
-    compiler spill cost the gate/up GEMM 3 % at the Mixtral shape)."""
+    and the addresses in 168 VGPRs: the gate/up GEMMs (plain, gathering,
+    packed, and the training forward's saving one) and the dgrad_down /
+    dgrad_in_add / wgrad kernels must compile without spills (a change to
+    the tile loop that made the compiler spill cost the gate/up GEMM 3 % at
+    the Mixtral shape)."""
     import shutil
 
     if shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists():
         pytest.skip("hipcc not available")
     kdir = Path(__file__).resolve().parent.parent / "astrai_amd" / "csrc" / "kernels"
     fwd = _device_kernel_metadata(kdir / "moe_gemm_mfma.hip", tmp_path)
-    # gemm_stream_kernel<gate_up=true, packed, save=false, gather>
-    inference_gu = {n: v for n, v in fwd.items() if re.search(r"gemm_stream_kernelILb1ELb[01]ELb0ELb[01]E", n)}
-    assert len(inference_gu) == 3, sorted(fwd)
-    for n, v in inference_gu.items():
+    # gemm_stream_kernel<gate_up=true, packed, save, gather>: the inference kernels and the saving one
+    gate_up = {n: v for n, v in fwd.items() if re.search(r"gemm_stream_kernelILb1ELb[01]ELb[01]ELb[01]E", n)}
+    assert len(gate_up) == 4, sorted(fwd)
+    for n, v in gate_up.items():
         assert v["vgpr"] <= 168 and v["spill"] == 0, (n, v)
     bwd = _device_kernel_metadata(kdir / "moe_gemm_bwd.hip", tmp_path)
     # Bwd::kDgradDown (0), kDgradInAdd (2), kWgrad (3), whole-tile launches (kTail false)
