@@ -58,12 +58,12 @@ PEAK_HBM_GBS = 8000.0
 # (TRAFFIC_SOURCE), not measured by this run: a counter pass needs the
 # profiler around the process.
 MEASURED_TRAFFIC_BYTES: dict[str, float] = {
-    "moe_bf16_d4096_f14336_e8_k2_t16384": (5992439.9 * 2 + 917620.2) * 1024,
-    "moe_bf16_d2048_f1408_e64_k6_t8192": (1200870.0 * 2 + 135200.3) * 1024,
-    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (1090051.2 * 2 + 135200.7) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t64": (1542838.4 * 2 + 1537.4) * 1024,
-    "moe_bf16_d4096_f1536_e128_k8_t1024": (1681990.6 * 2 + 24584.5) * 1024,
-    "moe_fp32_d512_f1024_e8_k2_t1024": (73290.9 * 2 + 8195.5) * 1024,
+    "moe_bf16_d4096_f14336_e8_k2_t16384": (5979173.2 * 2 + 917618.0) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192": (1192495.2 * 2 + 135201.3) * 1024,
+    "moe_bf16_d2048_f1408_e64_k6_t8192_zipf": (1069864.4 * 2 + 135200.6) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t64": (1543036.9 * 2 + 1538.1) * 1024,
+    "moe_bf16_d4096_f1536_e128_k8_t1024": (1682144.4 * 2 + 24587.0) * 1024,
+    "moe_fp32_d512_f1024_e8_k2_t1024": (73347.5 * 2 + 8195.6) * 1024,
 }
 
 
