@@ -68,7 +68,8 @@ MEASURED_TRAFFIC_BYTES: dict[str, float] = {
 
 
 TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE passes of bench.py on this workload, "
-                  "profiles/moe_layer_<workload>.md (a constant from that profiled run, not measured here)")
+                  "profiles/moe_layer_<workload>.md (a constant from that profiled run on another MI355X box, "
+                  "2026-12-02, scaled by a 1 GiB copy probe; not measured here)")
 
 
 def _parse():
